@@ -1,0 +1,118 @@
+/*
+ * onecomp-amd: C ABI of the MI355X (gfx950) quantized-linear hot path.
+ *
+ * Drop-in boundary for OneComp's quantized-linear inference path:
+ *   - Mixed-GPTQ  LinearMethod.apply()  (vllm_plugins/gptq/vllm_plugin.py:332-353 dispatches it
+ *     to vLLM's GPTQ/Marlin kernels; this library replaces those kernels), and
+ *   - DBF / MDBF  sign-factor matmuls   (vllm_plugins/dbf/vllm_plugin.py:275-328,
+ *     onecomp/quantizer/mdbf/mdbf_layer.py:307-344, :412-420).
+ *
+ * Conventions
+ *   - Every function returns 0 on success or a negative OC_ERR_* code; the message of the last
+ *     failure on the calling thread is returned by oc_last_error().
+ *   - All pointers are device pointers unless stated otherwise.  `stream` is a hipStream_t
+ *     (NULL = the default stream).  No entry point allocates device memory; work buffers are
+ *     passed in by the caller.  Launches are asynchronous unless a comment says otherwise.
+ *   - Activations, scales and outputs are 16-bit floats: OC_DTYPE_F16 (IEEE half) or
+ *     OC_DTYPE_BF16.  GPTQ scales are always fp16 (the checkpoint dtype).
+ *   - Layouts follow the OneComp checkpoint (AutoGPTQ layout): qweight [K*b/32, N] int32,
+ *     qzeros [G, N*b/32] int32, scales [G, N] fp16, g_idx [K] int32; DBF signs are uint8,
+ *     MSB first, flat row-major, padding bits = 1.
+ */
+#ifndef ONECOMP_AMD_H
+#define ONECOMP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OC_ABI_VERSION 1
+
+enum {
+  OC_OK = 0,
+  OC_ERR_INVALID = -1,     /* bad argument (null pointer, negative size, ...) */
+  OC_ERR_UNSUPPORTED = -2, /* unsupported bit width / group size / dtype */
+  OC_ERR_SHAPE = -3,       /* shape violates a layout requirement */
+  OC_ERR_HIP = -4,         /* a HIP runtime call failed */
+  OC_ERR_WORKSPACE = -5,   /* workspace or counter buffer too small */
+  OC_ERR_GIDX = -6         /* g_idx does not describe equal-size contiguous groups after sorting */
+};
+
+enum { OC_DTYPE_F16 = 0, OC_DTYPE_BF16 = 1 };
+
+/* Zero-point storage of qzeros (gptq_layer.py:543-557; checkpoint.py:217-221). */
+enum {
+  OC_ZERO_RAW = 0, /* return the stored fields untouched (parity tool only) */
+  OC_ZERO_V1 = 1,  /* checkpoint_format != "gptq_v2": z = (stored + 1) & (2^b - 1) */
+  OC_ZERO_V2 = 2   /* checkpoint_format == "gptq_v2": z = stored */
+};
+
+int oc_abi_version(void);
+const char* oc_last_error(void);
+
+/* ---------------------------------------------------------------- GPTQ parity tools -------- */
+
+/* codes[N, K] = unpacked qweight (int32 in [0, 2^b-1]).
+ * Replaces unpack_int_weights, onecomp/quantizer/gptq/gptq_layer.py:142-157 (_unpack_rows :86-126). */
+int oc_gptq_unpack_codes(const int32_t* qweight, int K, int N, int bits, int32_t* codes,
+                         void* stream);
+
+/* zeros[G, N] = unpacked qzeros, restored per zero_format (OC_ZERO_*).
+ * Replaces unpack_zeros gptq_layer.py:173-184 and the restore at gptq_layer.py:550-557. */
+int oc_gptq_unpack_zeros(const int32_t* qzeros, int G, int N, int bits, int zero_format,
+                         int32_t* zeros, void* stream);
+
+/* W[N, K] = RNE_dtype(fp32(scales[g_idx[k], n]) * (q[n, k] - z[g_idx[k], n])), bit-exact.
+ * g_idx may be NULL (then g = k / group_size, or 0 when group_size <= 0).
+ * Replaces the dequantisation of GPTQLinear.forward gptq_layer.py:536-569 and
+ * iter_gptq_layers + dequantize_layer onecomp/cpu/export/checkpoint.py:186-259. */
+int oc_gptq_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                    const int32_t* g_idx, int K, int N, int G, int bits, int group_size,
+                    int zero_format, int out_dtype, void* w, void* stream);
+
+/* ---------------------------------------------------------------- GPTQ load-time repack ----- */
+
+/* Sizes of the internal layout for a K x N layer at `bits`: packed weight bytes, padded K
+ * (multiple of 128, 256 or 512 depending on bits) and padded N (multiple of 16).  Host only. */
+int oc_gptq_layout(int K, int N, int bits, size_t* packed_bytes, int* k_pad, int* n_pad);
+
+/* Repack a checkpoint layer into the kernel layout.
+ *   packed : layout bytes from oc_gptq_layout
+ *   meta   : uint32 [G, n_pad]; low half = fp16 scale bits, high half = restored zero
+ *   perm   : int32 [K]; receives the stable argsort of g_idx (act-order).  May be NULL when
+ *            g_idx is NULL.  *perm_identity (host pointer, may be NULL) is set to 1 when the sort
+ *            is the identity, in which case the caller can pass perm = NULL to oc_gptq_gemm.
+ * With g_idx != NULL this call synchronizes `stream` to validate that the sorted g_idx forms G
+ * contiguous groups of group_size (OC_ERR_GIDX otherwise).
+ * Replaces vLLM GPTQLinearMethod.process_weights_after_loading (g_idx argsort + gptq_shuffle),
+ * reached via vllm_plugins/gptq/vllm_plugin.py:348-353. */
+int oc_gptq_prepare(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                    const int32_t* g_idx, int K, int N, int G, int bits, int group_size,
+                    int zero_format, void* packed, uint32_t* meta, int32_t* perm,
+                    int* perm_identity, void* stream);
+
+/* ---------------------------------------------------------------- GPTQ hot path ------------ */
+
+/* Workspace bytes oc_gptq_gemm needs for this call (host only). */
+size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int group_size, int has_perm);
+
+/* y[M, N] = x[M, K] @ dequant(W)^T (+ bias), fp32 accumulation, y in act_dtype.
+ * x row stride is K.  perm: int32 [K] from oc_gptq_prepare or NULL.  bias: [N] act_dtype or NULL.
+ * workspace: at least oc_gptq_workspace_bytes() bytes of device memory (may be NULL when that is
+ * 0); its contents need no initialisation and are dead after the call's kernels finish.
+ * Launches 1-3 kernels on `stream`; no host synchronisation, no allocation, no memset, so the
+ * call can be captured in a HIP graph.
+ * Replaces vLLM GPTQLinearMethod.apply -> ops.gptq_gemm (selected at vllm_plugin.py:348-353)
+ * and GPTQMarlinLinearMethod.apply (vllm_plugin.py:332-346). */
+int oc_gptq_gemm(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
+                 const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
+                 void* y, void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONECOMP_AMD_H */

@@ -1,0 +1,89 @@
+"""ctypes binding of the C ABI in ``include/onecomp_amd.h`` (``lib/liboc_quant.so``).
+
+The library is loaded after ``import torch`` so that it shares the HIP runtime
+torch already loaded (both use the soname ``libamdhip64.so.7``).  There is no
+fallback: if the library is missing, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("ONECOMP_AMD_LIB", os.path.join(_PKG, "lib", "liboc_quant.so"))
+
+c_int, c_size_t, c_void_p = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
+c_char_p = ctypes.c_char_p
+P = ctypes.c_void_p  # every device pointer travels as an untyped address
+c_int_p = ctypes.POINTER(ctypes.c_int)
+c_size_t_p = ctypes.POINTER(ctypes.c_size_t)
+
+# name -> (restype, argtypes); mirrors include/onecomp_amd.h one for one
+SIGNATURES = {
+    "oc_abi_version": (c_int, []),
+    "oc_last_error": (c_char_p, []),
+    "oc_gptq_unpack_codes": (c_int, [P, c_int, c_int, c_int, P, P]),
+    "oc_gptq_unpack_zeros": (c_int, [P, c_int, c_int, c_int, c_int, P, P]),
+    "oc_gptq_dequant": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P, P]),
+    "oc_gptq_layout": (c_int, [c_int, c_int, c_int, c_size_t_p, c_int_p, c_int_p]),
+    "oc_gptq_prepare": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P, P, P,
+                                c_int_p, P]),
+    "oc_gptq_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "oc_gptq_gemm": (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P, P,
+                             c_size_t, P]),
+}
+
+ABI_VERSION = 1
+OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
+OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2
+ERR_NAMES = {-1: "INVALID", -2: "UNSUPPORTED", -3: "SHAPE", -4: "HIP", -5: "WORKSPACE", -6: "GIDX"}
+
+
+class OCError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, code: int, fn: str, msg: str):
+        super().__init__(f"{fn} failed with OC_ERR_{ERR_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library (no GPU needed) and bind every declared symbol."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"onecomp-amd native library not found at {path}; build it with "
+                "`python -m onecompression_amd.build` (there is no CPU fallback)"
+            )
+        import torch  # noqa: F401  -- ensures torch's HIP runtime is the one in the process
+
+        lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        if lib.oc_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"ABI mismatch: library {lib.oc_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> int:
+    """Call a status-returning entry point and raise OCError on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise OCError(rc, name, lib.oc_last_error().decode(errors="replace"))
+    return rc
+
+
+def last_error() -> str:
+    return load().oc_last_error().decode(errors="replace")

@@ -1,0 +1,94 @@
+"""Seeded synthetic checkpoints and activations for the benchmark configs.
+
+Generated on the CPU with ``torch.Generator(device="cpu").manual_seed(seed)``
+so every consumer (GPU path, CPU baseline, tests) sees identical bytes, then
+copied to the requested device.  Uniform codes are produced directly as
+uniform random packed words: every bit of a packed word is an independent fair
+bit, so each b-bit code (including the 3-bit codes that straddle words) is
+uniform on [0, 2^b - 1], exactly as the configs ask.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+
+@dataclass
+class GPTQCase:
+    name: str
+    in_features: int
+    out_features: int
+    bits: int
+    group_size: int
+    act_order: bool
+    qweight: torch.Tensor  # int32 [K*b/32, N]
+    qzeros: torch.Tensor   # int32 [G, N*b/32] (stored v1 fields)
+    scales: torch.Tensor   # fp16 [G, N]
+    g_idx: Optional[torch.Tensor]  # int32 [K] or None
+
+    def weight_bytes(self) -> int:
+        n = self.qweight.numel() * 4 + self.qzeros.numel() * 4 + self.scales.numel() * 2
+        if self.g_idx is not None:
+            n += self.g_idx.numel() * 4
+        return n
+
+    def to(self, dev):
+        return GPTQCase(self.name, self.in_features, self.out_features, self.bits, self.group_size,
+                        self.act_order, self.qweight.to(dev), self.qzeros.to(dev),
+                        self.scales.to(dev), None if self.g_idx is None else self.g_idx.to(dev))
+
+
+def _words(gen, shape):
+    return torch.randint(-(2**31), 2**31, shape, generator=gen, dtype=torch.int64).to(torch.int32)
+
+
+def gptq_case(name, k, n, bits, group_size=128, act_order=False, seed=0) -> GPTQCase:
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    gs = k if group_size <= 0 else group_size
+    g = (k + gs - 1) // gs
+    qweight = _words(gen, (k * bits // 32, n))
+    qzeros = _words(gen, (g, n * bits // 32))
+    scales = (torch.randn((g, n), generator=gen).abs() * 0.02 + 1e-3).to(torch.float16)
+    g_idx = None
+    if act_order:
+        perm = torch.randperm(k, generator=gen)
+        g_idx = (torch.argsort(perm) // gs).to(torch.int32)
+    return GPTQCase(name, k, n, bits, group_size, act_order, qweight, qzeros, scales, g_idx)
+
+
+def activations(m, k, dtype=torch.float16, seed=1) -> torch.Tensor:
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randn((m, k), generator=gen).to(dtype)
+
+
+# BASELINE configs (shapes and bit widths) -------------------------------------------------
+CONFIG0 = [("linear", 4096, 4096, 4)]
+CONFIG1 = [  # Llama-3-8B decoder layer, Mixed-GPTQ per projection
+    ("q_proj", 4096, 4096, 4),
+    ("k_proj", 4096, 1024, 8),
+    ("v_proj", 4096, 1024, 8),
+    ("o_proj", 4096, 4096, 4),
+    ("gate_proj", 4096, 14336, 3),
+    ("up_proj", 4096, 14336, 3),
+    ("down_proj", 14336, 4096, 2),
+]
+CONFIG2 = [  # Qwen3-8B MLP, 3-bit act-order
+    ("gate_proj", 4096, 12288, 3),
+    ("up_proj", 4096, 12288, 3),
+    ("down_proj", 12288, 4096, 3),
+]
+CONFIG4 = [  # Qwen3-14B prefill, 4-bit, bf16 activations
+    ("qkv_proj", 5120, 7168, 4),
+    ("o_proj", 5120, 5120, 4),
+    ("gate_up_proj", 5120, 34816, 4),
+    ("down_proj", 17408, 5120, 4),
+]
+
+
+def config_cases(cfg: int, seed: int = 0):
+    spec = {0: CONFIG0, 1: CONFIG1, 2: CONFIG2, 4: CONFIG4}[cfg]
+    act = cfg == 2
+    return [gptq_case(name, k, n, b, 128, act, seed + i) for i, (name, k, n, b) in enumerate(spec)]

@@ -1,0 +1,165 @@
+"""GPU parity of the GPTQ path against the oracle (through the C ABI)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq as og
+from onecompression_amd import ops, synth
+from onecompression_amd import _native as N
+
+pytestmark = pytest.mark.gpu
+
+BITS = [2, 3, 4, 8]
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _case(k, n, bits, gs=128, act=False, seed=0):
+    return synth.gptq_case("t", k, n, bits, gs, act, seed)
+
+
+def _oracle_w(c, dtype, fmt="gptq"):
+    g = _np(c.g_idx) if c.g_idx is not None else og.default_g_idx(c.in_features, c.group_size)
+    return og.dequantize(_np(c.qweight), _np(c.qzeros), _np(c.scales), g, c.bits, fmt, dtype)
+
+
+def _rel(y, ref):
+    return float(np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_unpack_codes_bit_exact(dev, bits):
+    c = _case(256, 96 if bits != 3 else 64, bits, seed=bits)
+    got = _np(ops.gptq_unpack_codes(c.qweight.to(dev), bits))
+    want = og.unpack_int_weights(_np(c.qweight), bits, (c.out_features, c.in_features))
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("fmt", [N.OC_ZERO_RAW, N.OC_ZERO_V1, N.OC_ZERO_V2])
+def test_unpack_zeros_bit_exact(dev, bits, fmt):
+    c = _case(256, 128, bits, seed=10 + bits)
+    got = _np(ops.gptq_unpack_zeros(c.qzeros.to(dev), bits, c.out_features, fmt))
+    raw = og.unpack_zeros(_np(c.qzeros), bits, c.out_features)
+    want = raw if fmt == N.OC_ZERO_RAW else og.restore_zeros(raw, bits, "gptq" if fmt == 1 else "gptq_v2")
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs,act", [(128, False), (32, False), (-1, False), (128, True), (64, True)])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_dequant_bit_exact(dev, bits, gs, act, dtype):
+    c = _case(512, 64, bits, gs, act, seed=bits * 7 + (gs % 97))
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    cd = c.to(dev)
+    g = cd.g_idx
+    if g is None:
+        g = torch.from_numpy(og.default_g_idx(c.in_features, gs)).to(dev)
+    got = ops.gptq_dequant(cd.qweight, cd.qzeros, cd.scales, g, bits, gs, N.OC_ZERO_V1, td)
+    want = _oracle_w(c, dtype)
+    assert np.array_equal(_np(got.view(torch.int16)).view(np.uint16), want.view(np.uint16))
+
+
+def test_dequant_config0_full_size_bit_exact(dev):
+    c = synth.config_cases(0)[0]
+    cd = c.to(dev)
+    g = torch.from_numpy(og.default_g_idx(4096, 128)).to(dev)
+    got = ops.gptq_dequant(cd.qweight, cd.qzeros, cd.scales, g, 4, 128)
+    assert np.array_equal(_np(got).view(np.uint16), _oracle_w(c, "fp16").view(np.uint16))
+
+
+def _gemm_check(dev, c, m, dtype, bias=False, tol=1e-2, seed=3):
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    cd = c.to(dev)
+    prep = ops.gptq_prepare(cd.qweight, cd.qzeros, cd.scales, cd.g_idx, c.bits, c.group_size)
+    x = synth.activations(m, c.in_features, td, seed=seed)
+    b = (torch.randn(c.out_features) * 0.1).to(td) if bias else None
+    y = ops.gptq_gemm(x.to(dev), prep, None if b is None else b.to(dev))
+    torch.cuda.synchronize()
+    w = _oracle_w(c, dtype)
+    xb = _np(x.view(torch.int16)).view(np.uint16) if dtype == "bf16" else _np(x)
+    bb = None if b is None else (_np(b.view(torch.int16)).view(np.uint16) if dtype == "bf16" else _np(b))
+    ref = og.linear_ref(xb, w, dtype, bb)
+    got = _np(y.float())
+    assert got.shape == ref.shape
+    r = _rel(got, ref)
+    assert r <= tol, f"max rel err {r:.3e} > {tol}"
+    return r
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 40, 64])
+def test_gemm_small_m(dev, bits, m):
+    _gemm_check(dev, _case(1024, 256 if bits != 3 else 320, bits, seed=bits + m), m, "fp16")
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs,act", [(32, False), (64, False), (-1, False), (128, True)])
+def test_gemm_groups_and_act_order(dev, bits, gs, act):
+    _gemm_check(dev, _case(1024, 192, bits, gs, act, seed=bits), 3, "fp16", bias=True)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [1, 24, 100])
+def test_gemm_bf16(dev, bits, m):
+    _gemm_check(dev, _case(512, 128, bits, seed=40 + bits), m, "bf16", bias=True)
+
+
+def test_gemm_exact_zero_probe(dev):
+    """test_gptq_layer_pack.py:338-392 through the fused kernel: qweight=0,
+    scale=1, one-hot x -> columns with raw zero 0 give exactly 0, others -1."""
+    k = n = 128
+    for bits in BITS:
+        raw = np.ones((1, n), dtype=np.int32)
+        raw[:, :4] = 0
+        qw = torch.from_numpy(og.pack_int_weights(np.zeros((n, k), np.int32), bits)).to(dev)
+        qz = torch.from_numpy(og.pack_zeros(raw - 1, bits)).to(dev)
+        sc = torch.ones((1, n), dtype=torch.float16, device=dev)
+        prep = ops.gptq_prepare(qw, qz, sc, None, bits, -1)
+        x = torch.zeros((1, k), dtype=torch.float16, device=dev)
+        x[0, 0] = 1
+        y = ops.gptq_gemm(x, prep).float().cpu()[0]
+        assert torch.all(y[:4] == 0) and torch.all(y[4:] == -1), bits
+
+
+@pytest.mark.parametrize("idx", range(7))
+def test_gemm_config1_projection_m1(dev, idx):
+    c = synth.config_cases(1)[idx]
+    _gemm_check(dev, c, 1, "fp16")
+
+
+def test_gemm_config2_act_order_m16(dev):
+    c = synth.config_cases(2)[2]  # down 12288 -> 4096, 3-bit, act-order
+    _gemm_check(dev, c, 16, "fp16")
+
+
+def test_gemm_repeatable_split_k(dev, monkeypatch):
+    """The split-K path (forced) is deterministic and matches the unsplit one."""
+    c = synth.config_cases(1)[1].to(dev)  # k_proj 4096 -> 1024
+    prep = ops.gptq_prepare(c.qweight, c.qzeros, c.scales, None, c.bits, 128)
+    x = synth.activations(3, 4096).to(dev)
+    y1 = ops.gptq_gemm(x, prep).clone()
+    monkeypatch.setenv("OC_GEMV_S", "4")
+    prep._ws.clear()
+    y4 = ops.gptq_gemm(x, prep)
+    for _ in range(3):
+        assert torch.equal(ops.gptq_gemm(x, prep), y4)
+    torch.cuda.synchronize()
+    assert float((y4.float() - y1.float()).abs().max()) <= 1e-2 * float(y1.float().abs().max())
+    prep._ws.clear()
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("w,nt", [(4, 1), (8, 1), (16, 1), (4, 2), (8, 2), (16, 2)])
+def test_gemv_plan_variants(dev, monkeypatch, bits, w, nt):
+    """Every GEMV launch shape (waves per workgroup x n-tiles per wave), with
+    several k-units per wave, M = 1 and M = 7 (x rows bounced through LDS by a
+    subset of lanes)."""
+    monkeypatch.setenv("OC_GEMV_W", str(w))
+    monkeypatch.setenv("OC_GEMV_NT", str(nt))
+    c = _case(4096, 256 if bits != 3 else 320, bits, seed=60 + bits)
+    for m in (1, 7):
+        _gemm_check(dev, c, m, "fp16", bias=m == 7)
