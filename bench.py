@@ -69,14 +69,9 @@ def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes
     outs = [torch.empty((m, c.out_features), dtype=dtype, device=dev) for c in cases]
     step_bytes = sum(_gptq_bytes(c, m) for c in cases)
 
-    def step(i, ev=None):
-        preps = sets[i % len(sets)]
-        for j, (p, x, o) in enumerate(zip(preps, xs, outs)):
-            if ev is not None:
-                ev[j][0].record()
+    def step(i):
+        for p, x, o in zip(sets[i % len(sets)], xs, outs):
             ops.gptq_gemm(x, p, out=o)
-            if ev is not None:
-                ev[j][1].record()
 
     for i in range(max(warmup, len(sets))):
         step(i)
@@ -99,17 +94,22 @@ def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
 
-    # Per-kernel durations: HIP events around every launch on the launch
-    # stream, with the stream pre-loaded by a spin kernel so that the host
-    # enqueues all launches before the GPU reaches them.
-    events = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-               for _ in cases] for _ in range(steps)]
-    torch.cuda._sleep(int(2e8))
-    for i in range(steps):
-        step(warmup + i, events[i])
+    # Per-kernel durations: for each projection, HIP events on the launch
+    # stream around `steps` back-to-back launches of that kernel (rotating
+    # weight copies), with the stream pre-loaded by a spin kernel so that the
+    # host enqueues every launch before the GPU reaches them.
+    per_kernel_ms = []
+    torch.cuda._sleep(int(1e8))
+    evs = []
+    for j in range(len(cases)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            ops.gptq_gemm(xs[j], sets[(warmup + i) % len(sets)][j], out=outs[j])
+        e1.record()
+        evs.append((e0, e1))
     torch.cuda.synchronize()
-    per_kernel_ms = [statistics.mean(events[i][j][0].elapsed_time(events[i][j][1]) for i in range(steps))
-                     for j in range(len(cases))]
+    per_kernel_ms = [e0.elapsed_time(e1) / steps for e0, e1 in evs]
     kernels = []
     for c, t in zip(cases, per_kernel_ms):
         b = _gptq_bytes(c, m)
@@ -216,7 +216,7 @@ def main():
                    "weight_copies_rotated": r["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": f"k_skinny {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b",
+                     "kernel": f"k_gemv {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b",
                      "avg_us": round(dom["us"], 2)},
         "per_kernel": [{k: (round(v, 2) if isinstance(v, float) else v) for k, v in kk.items()}
                        for kk in r["kernels"]],

@@ -111,6 +111,43 @@ int oc_gptq_gemm(const void* x, int M, int K, int N, const void* packed, const u
                  const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
                  void* y, void* workspace, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- DBF / MDBF ---------------- */
+
+/* Sizes of the internal sign layout of an R x Kd +-1 factor (host only): packed bytes, padded
+ * reduction length and the k-blocks per lane load (1, 2 or 4). */
+int oc_dbf_layout(int R, int Kd, size_t* packed_bytes, int* k_pad, int* unit_k);
+
+/* out[R, Kd] int8 = +-1 signs of a checkpoint factor (uint8, MSB first, flat row-major, 1 -> +1).
+ * Replaces unpack_sign_bits vllm_plugins/dbf/modules/naive.py:9-42 and unpack_binary_factor
+ * onecomp/quantizer/dbf/dbf_layer.py:71-86 / mdbf_layer.py:86-103 (parity tool). */
+int oc_dbf_unpack_signs(const uint8_t* bp, int R, int Kd, int8_t* out, void* stream);
+
+/* Repack a checkpoint sign factor (R x Kd) into the kernel layout (oc_dbf_layout bytes).
+ * Replaces the per-call unpack of DBFLinearMethod._apply_naive (vllm_plugin.py:275-294) and the
+ * GemLite packing of process_weights_after_loading (vllm_plugin.py:232-273). */
+int oc_dbf_prepare(const uint8_t* bp, int R, int Kd, void* packed, void* stream);
+
+/* One term of a sign matmul: post[n] * sum_k S[n, k] * (pre[k] * in[m, k]).
+ * packed: oc_dbf_prepare output for S (R x Kd); in: [M, ld_in] activations (ld_in >= Kd, a
+ * multiple of 8, 16-byte aligned rows, entries Kd..ld_in-1 zero); pre (16-byte aligned, Kd entries
+ * zero-padded to a multiple of 8) and post [R] may be NULL (= ones). */
+typedef struct {
+  const void* packed;
+  const void* in;
+  const void* pre;
+  const void* post;
+  int Kd;
+  int ld_in;
+} oc_sign_term;
+
+/* out[m, n] = sum over terms of the term above (+ bias[n]) for n < R, rounded once to act_dtype;
+ * columns R <= n < fill_to are written as 0.  n_terms <= 4; all terms need the same unit size.
+ * A DBF stage is one term (vllm_plugin.py:275-294: stage 1 pre=scaling0, post=scaling2; stage 2
+ * post=scaling4), the P paths of MDBF stage 2 are P terms summed in one call
+ * (mdbf_layer.py:338-344, :412-420).  Replaces DBFLinearMethod._apply_naive/_apply_gemlite. */
+int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R, int act_dtype,
+                 const void* bias, void* out, int ld_out, int fill_to, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,10 @@ SIGNATURES = {
     "oc_gptq_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "oc_gptq_gemm": (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P, P,
                              c_size_t, P]),
+    "oc_dbf_layout": (c_int, [c_int, c_int, c_size_t_p, c_int_p, c_int_p]),
+    "oc_dbf_unpack_signs": (c_int, [P, c_int, c_int, P, P]),
+    "oc_dbf_prepare": (c_int, [P, c_int, c_int, P, P]),
+    "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P]),
 }
 
 ABI_VERSION = 1

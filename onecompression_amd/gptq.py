@@ -1,0 +1,311 @@
+"""Mixed-GPTQ quantization config and linear method backed by the HIP kernels.
+
+Drop-in for vllm_plugins/gptq (registered as ``"mixed_gptq"``):
+
+- :class:`MixedGPTQConfig` keeps the reference's config parsing and per-module
+  dispatch (vllm_plugins/gptq/vllm_plugin.py:83-365): ``quantization_bits``
+  (or legacy ``layer_bits``), group size priority direct > ``params`` >
+  global, ``desc_act``, ``sym``, ``lm_head`` and ``checkpoint_format``
+  defaulting to ``"gptq_v2"`` when absent.  bits 0 or no entry -> unquantized;
+  fused modules whose constituents differ -> ``ValueError``.
+- Where the reference hands 4/8-bit symmetric layers to vLLM's Marlin kernel
+  and everything else to vLLM's Exllama kernel (:332-353,
+  vllm_plugins/gptq/constants.py:12-31), every GPTQ layer here goes to
+  :class:`GPTQLinearMethod`, one HIP kernel family for 2/3/4/8 bits with or
+  without act-order.
+- :class:`GPTQLinearMethod` registers the checkpoint tensors under the same
+  names and shapes (``qweight`` [K*b/32, N] int32, ``qzeros`` [G, N*b/32]
+  int32, ``scales`` [G, N], ``g_idx`` [K] int32), repacks them once in
+  ``process_weights_after_loading`` and runs ``apply`` as one C-ABI call.
+
+Deviation kept on purpose: ``scales`` are stored in fp16, the checkpoint
+dtype, also for bf16 models, so the dequantised weight equals OneComp's own
+``RNE(fp32(s) * (q - z))`` bit for bit.
+"""
+
+from __future__ import annotations
+
+import logging
+import re
+from fractions import Fraction
+from typing import Any, Dict, List, Optional
+
+import torch
+
+from . import ops
+from . import _native as N
+from .module_utils import (
+    lookup_module_config,
+    parse_layer_and_module,
+    validate_quant_config_within_shard,
+)
+from .rotation import RotationMetadata, maybe_wrap_rotation_method
+from .vllm_compat import (
+    FusedMoE,
+    LinearBase,
+    LinearMethodBase,
+    QuantizationConfig,
+    UnquantizedLinearMethod,
+    register_quantization_config,
+    set_weight_attrs,
+)
+
+logger = logging.getLogger(__name__)
+
+SUPPORTED_BITS = (2, 3, 4, 8)
+_MOE_EXPERT_CFG_RE = re.compile(r"(?:^|\.)experts\.\d+\.")
+
+
+class GPTQLayerConfig:
+    """Per-layer GPTQ parameters handed to :class:`GPTQLinearMethod`."""
+
+    def __init__(self, bits: int, group_size: int, desc_act: bool, sym: bool,
+                 checkpoint_format: str):
+        if bits not in SUPPORTED_BITS:
+            raise ValueError(f"GPTQ bits must be one of {SUPPORTED_BITS}, got {bits}")
+        self.weight_bits = bits
+        self.group_size = group_size
+        self.desc_act = desc_act
+        self.sym = sym
+        self.checkpoint_format = checkpoint_format
+        self.pack_factor = Fraction(32, bits)
+
+    @property
+    def zero_format(self) -> int:
+        return N.OC_ZERO_V2 if self.checkpoint_format == "gptq_v2" else N.OC_ZERO_V1
+
+    def __repr__(self):
+        return (f"GPTQLayerConfig(bits={self.weight_bits}, group_size={self.group_size}, "
+                f"desc_act={self.desc_act}, checkpoint_format={self.checkpoint_format})")
+
+
+def _shard_offsets(output_partition_sizes: List[int]):
+    offs, c = [], 0
+    for s in output_partition_sizes:
+        offs.append(c)
+        c += s
+    return offs
+
+
+def _shard_index(shard_id: Any, n_parts: int) -> int:
+    if shard_id is None:
+        return 0
+    if isinstance(shard_id, int):
+        return shard_id
+    mapping = {"q": 0, "k": 1, "v": 2}
+    if isinstance(shard_id, str) and shard_id in mapping and mapping[shard_id] < n_parts:
+        return mapping[shard_id]
+    raise ValueError(f"Unknown shard id: {shard_id}")
+
+
+class GPTQLinearMethod(LinearMethodBase):
+    """Linear method for one GPTQ layer (replaces vLLM's GPTQ/Marlin methods)."""
+
+    def __init__(self, quant_config: GPTQLayerConfig):
+        self.quant_config = quant_config
+
+    def create_weights(self, layer: torch.nn.Module, input_size_per_partition: int,
+                       output_partition_sizes: List[int], input_size: int, output_size: int,
+                       params_dtype: torch.dtype, **extra_weight_attrs):
+        cfg = self.quant_config
+        bits = cfg.weight_bits
+        k = input_size_per_partition
+        n = sum(output_partition_sizes)
+        gs = cfg.group_size if cfg.group_size != -1 else input_size
+        if k % 32:
+            raise ValueError(f"input size {k} must be a multiple of 32 for GPTQ packing")
+        if (n * bits) % 32 or any((p * bits) % 32 for p in output_partition_sizes):
+            raise ValueError(f"output sizes {output_partition_sizes} x {bits} bits must pack into int32")
+        if gs % 32:
+            raise ValueError(f"group_size {cfg.group_size} must be a multiple of 32 (or -1)")
+        groups = (k + gs - 1) // gs
+        offs = _shard_offsets(output_partition_sizes)
+        loader = extra_weight_attrs.pop("weight_loader", None)
+
+        def make_loader(out_dim: Optional[int], pack: int):
+            def _load(param, loaded_weight: torch.Tensor, loaded_shard_id: Any = None):
+                # g_idx (no output dim) is shared by every shard of a fused module
+                if out_dim is None or len(output_partition_sizes) == 1 or loaded_shard_id is None:
+                    param.data.copy_(loaded_weight)
+                    return
+                i = _shard_index(loaded_shard_id, len(output_partition_sizes))
+                start, size = offs[i] // pack, output_partition_sizes[i] // pack
+                param.data.narrow(out_dim, start, size).copy_(loaded_weight)
+
+            return loader if loader is not None else _load
+
+        qweight = torch.nn.Parameter(torch.empty(k * bits // 32, n, dtype=torch.int32), requires_grad=False)
+        set_weight_attrs(qweight, {"input_dim": 0, "output_dim": 1, "packed_dim": 0,
+                                   "pack_factor": cfg.pack_factor, "weight_loader": make_loader(1, 1),
+                                   **extra_weight_attrs})
+        g_idx = torch.nn.Parameter(torch.tensor([i // gs for i in range(k)], dtype=torch.int32),
+                                   requires_grad=False)
+        set_weight_attrs(g_idx, {"input_dim": 0, "ignore_warning": True,
+                                 "weight_loader": make_loader(None, 1), **extra_weight_attrs})
+        qzeros = torch.nn.Parameter(torch.empty(groups, n * bits // 32, dtype=torch.int32),
+                                    requires_grad=False)
+        set_weight_attrs(qzeros, {"input_dim": 0, "output_dim": 1, "packed_dim": 1,
+                                  "pack_factor": cfg.pack_factor,
+                                  "weight_loader": _zero_loader(loader, offs, output_partition_sizes, bits),
+                                  **extra_weight_attrs})
+        scales = torch.nn.Parameter(torch.empty(groups, n, dtype=torch.float16), requires_grad=False)
+        set_weight_attrs(scales, {"input_dim": 0, "output_dim": 1,
+                                  "weight_loader": make_loader(1, 1), **extra_weight_attrs})
+        layer.register_parameter("qweight", qweight)
+        layer.register_parameter("g_idx", g_idx)
+        layer.register_parameter("qzeros", qzeros)
+        layer.register_parameter("scales", scales)
+        layer._oc_gptq = {"in": k, "out": n, "groups": groups, "gs": gs,
+                          "parts": list(output_partition_sizes)}
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        cfg = self.quant_config
+        dev = layer.qweight.device
+        if dev.type != "cuda":
+            raise RuntimeError("GPTQLinearMethod needs the layer on a HIP device before "
+                               "process_weights_after_loading")
+        scales = layer.scales.data
+        if scales.dtype != torch.float16:
+            scales = scales.to(torch.float16)
+        g_idx = layer.g_idx.data.to(torch.int32).contiguous()
+        if not cfg.desc_act:
+            gs = layer._oc_gptq["gs"]
+            expected = torch.arange(g_idx.numel(), device=dev, dtype=torch.int32) // gs
+            if torch.equal(g_idx, expected):
+                g_idx = None
+        layer._oc_prep = ops.gptq_prepare(layer.qweight.data.contiguous(), layer.qzeros.data.contiguous(),
+                                          scales.contiguous(), g_idx, cfg.weight_bits,
+                                          cfg.group_size, cfg.zero_format)
+
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor,
+              bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        prep = getattr(layer, "_oc_prep", None)
+        if prep is None:
+            raise RuntimeError("GPTQ layer used before process_weights_after_loading")
+        if bias is not None and bias.dtype != x.dtype:
+            bias = bias.to(x.dtype)
+        return ops.gptq_gemm(x, prep, bias)
+
+
+def _zero_loader(loader, offs, parts, bits):
+    """qzeros are packed along N: shard i occupies columns offs[i]*b/32 ..."""
+    if loader is not None:
+        return loader
+
+    def _load(param, loaded_weight: torch.Tensor, loaded_shard_id: Any = None):
+        if len(parts) == 1 or loaded_shard_id is None:
+            param.data.copy_(loaded_weight)
+            return
+        i = _shard_index(loaded_shard_id, len(parts))
+        start, size = offs[i] * bits // 32, parts[i] * bits // 32
+        param.data.narrow(1, start, size).copy_(loaded_weight)
+
+    return _load
+
+
+@register_quantization_config("mixed_gptq")
+class MixedGPTQConfig(QuantizationConfig):
+    """``quant_method: mixed_gptq`` (vllm_plugins/gptq/vllm_plugin.py:83-365)."""
+
+    def __init__(self, quantization_bits, group_size=-1, desc_act=False, sym=False,
+                 lm_head_quantized=False, checkpoint_format="gptq_v2",
+                 rotation_metadata: Optional[RotationMetadata] = None):
+        super().__init__()
+        self.quantization_bits = quantization_bits
+        self.group_size = group_size
+        self.desc_act = desc_act
+        self.sym = sym
+        self.lm_head_quantized = lm_head_quantized
+        self.checkpoint_format = checkpoint_format
+        self.rotation_metadata = rotation_metadata if rotation_metadata is not None else RotationMetadata()
+        bits, methods = set(), set()
+        for layer_cfg in quantization_bits:
+            for mod_cfg in layer_cfg.values():
+                bits.add(mod_cfg.get("bits", 0))
+                methods.add(mod_cfg.get("method", "gptq"))
+        logger.info("MixedGPTQConfig: %d layers, bits=%s, methods=%s", len(quantization_bits),
+                    sorted(bits), sorted(methods))
+
+    def __repr__(self):
+        return (f"MixedGPTQConfig(layers={len(self.quantization_bits)}, "
+                f"group_size={self.group_size}, desc_act={self.desc_act})")
+
+    @classmethod
+    def get_name(cls) -> str:
+        return "mixed_gptq"
+
+    @classmethod
+    def get_supported_act_dtypes(cls) -> List[torch.dtype]:
+        return [torch.half, torch.bfloat16]
+
+    @classmethod
+    def get_min_capability(cls) -> int:
+        return 60
+
+    @staticmethod
+    def get_config_filenames() -> List[str]:
+        return ["quantize_config.json"]
+
+    @classmethod
+    def from_config(cls, config: Dict[str, Any]) -> "MixedGPTQConfig":
+        quantization_bits = config.get("quantization_bits", [])
+        if not quantization_bits and "layer_bits" in config:
+            quantization_bits = [{"_all": {"bits": b, "method": "gptq"}} for b in config["layer_bits"]]
+        return cls(quantization_bits=quantization_bits,
+                   group_size=config.get("group_size", -1),
+                   desc_act=config.get("desc_act", False),
+                   sym=config.get("sym", False),
+                   lm_head_quantized=config.get("lm_head", False),
+                   checkpoint_format=config.get("checkpoint_format", "gptq_v2"),
+                   rotation_metadata=RotationMetadata.from_quant_config(config))
+
+    def maybe_update_config(self, model_name, hf_config=None, revision=None):
+        """No-op: per-module dispatch comes from ``quantization_bits`` (vllm_plugin.py:213-218)."""
+
+    def resolve_group_size(self, mod_cfg: Optional[Dict]) -> int:
+        """Per-module direct > ``params`` > global (vllm_plugin.py:165-173)."""
+        if mod_cfg is not None:
+            if mod_cfg.get("group_size") is not None:
+                return mod_cfg["group_size"]
+            extra = mod_cfg.get("params", {})
+            if isinstance(extra, dict) and extra.get("group_size") is not None:
+                return extra["group_size"]
+        return self.group_size
+
+    def _unquantized(self, prefix: str):
+        return maybe_wrap_rotation_method(UnquantizedLinearMethod(), prefix=prefix,
+                                          metadata=self.rotation_metadata)
+
+    def get_quant_method(self, layer: torch.nn.Module, prefix: str):
+        if FusedMoE is not None and isinstance(layer, FusedMoE):
+            raise NotImplementedError(
+                "onecomp-amd serves dense GPTQ linears only; the GPT-OSS / Qwen MoE WNA16 "
+                "expert path (vllm_plugins/gptq/gptoss_wna16_moe.py) is not part of this build")
+        if not isinstance(layer, LinearBase):
+            return None
+        layer_idx, suffix = parse_layer_and_module(prefix)
+        if layer_idx is None:
+            return self._unquantized(prefix)
+        mod_cfg = lookup_module_config(self.quantization_bits, layer_idx, suffix)
+        if mod_cfg is None:
+            return self._unquantized(prefix)
+        if not validate_quant_config_within_shard(self.quantization_bits, layer_idx, suffix):
+            raise ValueError(f"Detected some but not all shards of {prefix} are quantized. "
+                             "All shards of fused layers to have the same precision.")
+        bits = mod_cfg.get("bits", 0)
+        method = mod_cfg.get("method", "gptq")
+        if bits == 0:
+            return self._unquantized(prefix)
+        if method == "gptq" and int(bits) in SUPPORTED_BITS:
+            cfg = GPTQLayerConfig(int(bits), self.resolve_group_size(mod_cfg), self.desc_act,
+                                  bool(self.sym), self.checkpoint_format)
+            return maybe_wrap_rotation_method(GPTQLinearMethod(cfg), prefix=prefix,
+                                              metadata=self.rotation_metadata)
+        logger.warning("mixed_gptq: unsupported method=%s bits=%s at %s, falling back to unquantized",
+                       method, bits, prefix)
+        return self._unquantized(prefix)
+
+
+def register_vllm_plugin():
+    """vLLM ``general_plugins`` entry point (vllm_plugin.py:368-373)."""
+    register_quantization_config(MixedGPTQConfig)

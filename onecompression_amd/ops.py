@@ -27,7 +27,7 @@ def _stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
-def _need(t: torch.Tensor, name: str, dtype, shape=None, dev=None):
+def _need(t: torch.Tensor, name: str, dtype, shape=None, dev=None, align: int = 16):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
     if t.device.type != "cuda":
@@ -40,8 +40,8 @@ def _need(t: torch.Tensor, name: str, dtype, shape=None, dev=None):
         raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
-    if t.data_ptr() % 16:
-        raise ValueError(f"{name} must be 16-byte aligned")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name} must be {align}-byte aligned")
 
 
 # ----------------------------------------------------------------- parity tools

@@ -1,0 +1,157 @@
+"""vLLM plugin base classes, or local stand-ins when vLLM is not installed.
+
+When ``vllm`` is importable the real ``QuantizationConfig``,
+``LinearMethodBase``, ``LinearBase``, ``UnquantizedLinearMethod``,
+``set_weight_attrs`` and ``register_quantization_config`` are re-exported, so
+the configs in this package register with a real vLLM exactly like
+``vllm_plugins/gptq`` and ``vllm_plugins/dbf`` do (pyproject.toml:105-107).
+Otherwise minimal stand-ins with the same method names keep the plugin
+classes importable and testable (vLLM is an optional dependency here).
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, List, Optional
+
+import torch
+import torch.nn.functional as F
+
+try:  # pragma: no cover - exercised only where vLLM is installed
+    from vllm.model_executor.layers.linear import (  # type: ignore
+        LinearBase,
+        LinearMethodBase,
+        UnquantizedLinearMethod,
+    )
+    from vllm.model_executor.layers.quantization import register_quantization_config  # type: ignore
+    from vllm.model_executor.layers.quantization.base_config import (  # type: ignore
+        QuantizationConfig,
+        QuantizeMethodBase,
+    )
+    from vllm.model_executor.utils import set_weight_attrs  # type: ignore
+
+    try:
+        from vllm.model_executor.layers.fused_moe import FusedMoE  # type: ignore
+    except Exception:  # noqa: BLE001
+        FusedMoE = None
+    HAS_VLLM = True
+except Exception:  # noqa: BLE001 - any import failure means "no vLLM"
+    HAS_VLLM = False
+    FusedMoE = None
+
+    class QuantizeMethodBase:
+        """Stand-in for vllm...base_config.QuantizeMethodBase."""
+
+        def create_weights(self, layer: torch.nn.Module, *args, **kwargs):
+            raise NotImplementedError
+
+        def apply(self, layer: torch.nn.Module, *args, **kwargs) -> torch.Tensor:
+            raise NotImplementedError
+
+        def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+            return None
+
+    class LinearMethodBase(QuantizeMethodBase):
+        """Stand-in for vllm...linear.LinearMethodBase."""
+
+    class QuantizationConfig:
+        """Stand-in for vllm...base_config.QuantizationConfig."""
+
+        def __init__(self):
+            self.packed_modules_mapping: Dict[str, List[str]] = {}
+
+        @classmethod
+        def get_name(cls) -> str:
+            raise NotImplementedError
+
+        @classmethod
+        def get_supported_act_dtypes(cls) -> List[torch.dtype]:
+            raise NotImplementedError
+
+        @classmethod
+        def get_min_capability(cls) -> int:
+            raise NotImplementedError
+
+        @staticmethod
+        def get_config_filenames() -> List[str]:
+            raise NotImplementedError
+
+        @classmethod
+        def from_config(cls, config: Dict[str, Any]) -> "QuantizationConfig":
+            raise NotImplementedError
+
+        def get_quant_method(self, layer: torch.nn.Module, prefix: str):
+            raise NotImplementedError
+
+    class LinearBase(torch.nn.Module):
+        """Minimal linear layer in vLLM's style: the quant method owns the params.
+
+        ``output_partition_sizes`` lists the fused parts (e.g. q, k, v).
+        """
+
+        def __init__(self, input_size: int, output_size: int, bias: bool = False,
+                     params_dtype: torch.dtype = torch.float16,
+                     quant_config: Optional["QuantizationConfig"] = None, prefix: str = "",
+                     output_partition_sizes: Optional[List[int]] = None):
+            super().__init__()
+            self.input_size = input_size
+            self.output_size = output_size
+            self.params_dtype = params_dtype
+            self.prefix = prefix
+            self.output_partition_sizes = list(output_partition_sizes or [output_size])
+            if quant_config is None:
+                self.quant_method = UnquantizedLinearMethod()
+            else:
+                self.quant_method = quant_config.get_quant_method(self, prefix)
+            if self.quant_method is None:
+                self.quant_method = UnquantizedLinearMethod()
+            self.quant_method.create_weights(self, input_size, self.output_partition_sizes,
+                                             input_size, output_size, params_dtype)
+            if bias:
+                self.bias = torch.nn.Parameter(torch.zeros(output_size, dtype=params_dtype),
+                                               requires_grad=False)
+            else:
+                self.register_parameter("bias", None)
+
+        def forward(self, x: torch.Tensor) -> torch.Tensor:
+            return self.quant_method.apply(self, x, self.bias)
+
+    class UnquantizedLinearMethod(LinearMethodBase):
+        """Stand-in for vllm...linear.UnquantizedLinearMethod (dense F.linear)."""
+
+        def create_weights(self, layer, input_size_per_partition, output_partition_sizes,
+                           input_size, output_size, params_dtype, **extra_weight_attrs):
+            w = torch.nn.Parameter(torch.empty(sum(output_partition_sizes), input_size_per_partition,
+                                               dtype=params_dtype), requires_grad=False)
+            set_weight_attrs(w, {"input_dim": 1, "output_dim": 0, **extra_weight_attrs})
+            layer.register_parameter("weight", w)
+
+        def apply(self, layer, x, bias=None):
+            return F.linear(x, layer.weight, bias)
+
+    def set_weight_attrs(weight: torch.Tensor, weight_attrs: Optional[Dict[str, Any]]) -> None:
+        if weight_attrs is None:
+            return
+        for key, value in weight_attrs.items():
+            if hasattr(weight, key) and key != "weight_loader":
+                raise AttributeError(f"Overwriting existing tensor attribute: {key}")
+            setattr(weight, key, value)
+
+    _REGISTRY: Dict[str, type] = {}
+
+    def register_quantization_config(name_or_cls):
+        """Decorator/func registering a QuantizationConfig under its name (local registry)."""
+
+        def _reg(cls):
+            _REGISTRY[cls.get_name()] = cls
+            return cls
+
+        if isinstance(name_or_cls, str):
+            return _reg
+        return _reg(name_or_cls)
+
+
+def registered_configs() -> Dict[str, type]:
+    """Quantization configs registered through the local stand-in registry."""
+    if HAS_VLLM:  # pragma: no cover
+        return {}
+    return dict(_REGISTRY)

@@ -1,0 +1,147 @@
+"""GPU parity of the DBF / MDBF sign path against the oracle (through the C ABI)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dbf as od
+from oracle import gptq as og
+from onecompression_amd import dbf as D
+from onecompression_amd import dbf_ops
+from onecompression_amd.vllm_compat import HAS_VLLM, LinearBase
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _rel(y, ref):
+    return float(np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def _factors(k, n, seed, bits=1.0):
+    rng = np.random.default_rng(seed)
+    r = od.mid_features(bits, k, n)
+    bp1 = od.pack_binary(rng.choice([-1, 1], size=(r, k)))
+    bp3 = od.pack_binary(rng.choice([-1, 1], size=(n, r)))
+    s0, s2, s4 = [(np.abs(rng.normal(0, 0.05, d)) + 1e-3).astype(np.float16) for d in (k, r, n)]
+    return r, bp1, bp3, s0, s2, s4
+
+
+def test_unpack_known_answers(dev):
+    got = dbf_ops.unpack_signs(_t(np.array([0b11001100, 0b00110011], np.uint8), dev), 2, 8).cpu().numpy()
+    assert got.tolist() == [[1, 1, -1, -1, 1, 1, -1, -1], [-1, -1, 1, 1, -1, -1, 1, 1]]
+    got = dbf_ops.unpack_signs(_t(np.array([0b10101010], np.uint8), dev), 1, 8).cpu().numpy()
+    assert got.tolist() == [[1, -1, 1, -1, 1, -1, 1, -1]]
+
+
+@pytest.mark.parametrize("shape", [(5, 7), (13, 11), (3185, 64), (40, 3185)])
+def test_unpack_bit_exact(dev, shape):
+    rng = np.random.default_rng(shape[0])
+    m = rng.choice([-1, 1], size=shape).astype(np.int8)
+    p = od.pack_binary(m)
+    got = dbf_ops.unpack_signs(_t(p, dev), *shape).cpu().numpy()
+    assert np.array_equal(got, m) and np.array_equal(got, od.unpack_binary_factor(p, shape))
+
+
+def test_sign_matmul_known_answer(dev):
+    """test_dbf_naive.py:110-151 through the kernel: [[-4, 4], [4, -4]]."""
+    f = dbf_ops.sign_prepare(_t(np.array([0b10101010, 0b01010101], np.uint8), dev), 2, 8)
+    x = torch.tensor([[1, 2, 3, 4, 5, 6, 7, 8], [8, 7, 6, 5, 4, 3, 2, 1]], dtype=torch.float16, device=dev)
+    out = torch.empty((2, 8), dtype=torch.float16, device=dev)
+    dbf_ops.sign_gemm([(f, x, None, None)], 2, 2, torch.float16, out, 8)
+    assert out[:, :2].float().cpu().tolist() == [[-4, 4], [4, -4]]
+
+
+@pytest.mark.parametrize("k,n,m", [(256, 192, 1), (256, 192, 3), (640, 256, 16), (512, 384, 37),
+                                   (4096, 14336, 1), (14336, 4096, 1), (4096, 14336, 32)])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_dbf_forward(dev, k, n, m, dtype):
+    if dtype == "bf16" and k * n > 4096 * 4096:
+        pytest.skip("bf16 covered at small shapes")
+    r, bp1, bp3, s0, s2, s4 = _factors(k, n, k + n + m)
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(td)
+    prep = dbf_ops.dbf_prepare(_t(s0, dev), _t(bp1, dev), _t(s2, dev), _t(bp3, dev), _t(s4, dev), k, r, n)
+    y = dbf_ops.dbf_forward(x.to(dev), [prep]).float().cpu().numpy()
+    if dtype == "bf16":  # the reference casts the fp16 scalings to x.dtype (vllm_plugin.py:286-292)
+        xn = x.view(torch.int16).numpy().view(np.uint16)
+        sc = [og.f32_to_bf16_bits(v.astype(np.float32)) for v in (s0, s2, s4)]
+    else:
+        xn, sc = x.numpy(), [s0, s2, s4]
+    ref = od.dbf_forward(xn, sc[0], bp1, sc[1], bp3, sc[2], k, r, n, dtype=dtype)
+    tol = 1e-2 if dtype == "fp16" else 2e-2
+    assert _rel(y, ref) <= tol, _rel(y, ref)
+
+
+def test_dbf_all_plus_signs_fused_parts(dev):
+    """test_dbf_gemlite_fallback.py:274-329 through the kernels: all signs +1,
+    distinct per-part scalings, three fused parts; allclose(atol=rtol=1e-2)."""
+    k, mid, n_out, parts, batch = 64, 32, 48, 3, 4
+    s0 = torch.stack([torch.linspace(0.5, 1.5, k, dtype=torch.float16) * (1.0 + 0.1 * p) for p in range(parts)])
+    s2 = torch.linspace(0.5, 1.5, mid * parts, dtype=torch.float16)
+    s4 = torch.linspace(0.5, 1.5, n_out * parts, dtype=torch.float16)
+    bp1 = torch.full(((mid * k + 7) // 8,), 0xFF, dtype=torch.uint8)
+    bp3 = torch.full(((n_out * mid + 7) // 8,), 0xFF, dtype=torch.uint8)
+    preps = [dbf_ops.dbf_prepare(s0[p].to(dev), bp1.to(dev), s2[p * mid:(p + 1) * mid].to(dev), bp3.to(dev),
+                                 s4[p * n_out:(p + 1) * n_out].to(dev), k, mid, n_out) for p in range(parts)]
+    x = torch.randn(batch, k, generator=torch.Generator().manual_seed(0))
+    y = dbf_ops.dbf_forward(x.half().to(dev), preps).float().cpu()
+    exp = []
+    for p in range(parts):
+        h = (x.half().float() * s0[p].float()) @ torch.ones(mid, k).t()
+        h = h * s2[p * mid:(p + 1) * mid].float()
+        exp.append((h @ torch.ones(n_out, mid).t()) * s4[p * n_out:(p + 1) * n_out].float())
+    exp = torch.cat(exp, dim=-1)
+    assert y.shape == (batch, n_out * parts)
+    assert torch.allclose(y, exp, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.skipif(HAS_VLLM, reason="layer built with the local LinearBase stand-in")
+def test_dbf_plugin_layer_fused_qkv(dev):
+    qb = [{f"self_attn.{p}_proj": {"bits": 1.0, "method": "dbf"} for p in "qkv"}]
+    cfg = D.DbfConfig.from_config({"quantization_bits": qb})
+    k, parts = 256, [256, 64, 64]
+    layer = LinearBase(k, sum(parts), bias=True, quant_config=cfg, prefix="model.layers.0.self_attn.qkv_proj",
+                       output_partition_sizes=parts)
+    ref_parts, rng = [], np.random.default_rng(1)
+    for i, (sid, n) in enumerate(zip("qkv", parts)):
+        r, bp1, bp3, s0, s2, s4 = _factors(k, n, 10 + i)
+        assert r == layer._dbf_meta["mid_sizes"][i]
+        for name, val in (("scaling0", s0), ("scaling2", s2), ("scaling4", s4), ("bp1", bp1), ("bp3", bp3)):
+            p = getattr(layer, name)
+            p.weight_loader(p, torch.from_numpy(val), sid)
+        ref_parts.append((r, bp1, bp3, s0, s2, s4, n))
+    bias = rng.normal(0, 0.01, sum(parts)).astype(np.float16)
+    layer.bias.data.copy_(torch.from_numpy(bias))
+    layer.to(dev)
+    layer.quant_method.process_weights_after_loading(layer)
+    x = torch.randn(3, k, generator=torch.Generator().manual_seed(2)).half()
+    y = layer(x.to(dev)).float().cpu().numpy()
+    ref = np.concatenate([od.dbf_forward(x.numpy(), s0, bp1, s2, bp3, s4, k, r, n)
+                          for (r, bp1, bp3, s0, s2, s4, n) in ref_parts], axis=1) + bias.astype(np.float32)
+    assert _rel(y, ref) <= 1e-2
+
+
+def _mdbf_path(n, m, r, l, seed):
+    rng = np.random.default_rng(seed)
+    amp = lambda *s: (np.abs(rng.normal(0, 0.3, s)) + 1e-2).astype(np.float16)  # noqa: E731
+    return dict(A_sign_packed=od.pack_binary(rng.choice([-1, 1], size=(n, r))), A_shape=(n, r),
+                B_sign_packed=od.pack_binary(rng.choice([-1, 1], size=(r, m))), B_shape=(r, m),
+                A_amp=amp(n, l), B_amp=amp(m, l), Q_U_amp=amp(r, l), Q_V_amp=amp(r, l))
+
+
+@pytest.mark.parametrize("P,l,m_rows", [(2, 1, 1), (2, 1, 32), (1, 2, 4), (2, 2, 1)])
+def test_mdbf_forward(dev, P, l, m_rows):
+    n, m = 384, 256
+    r = od.mid_features(1.0, m, n)
+    paths = [_mdbf_path(n, m, r, l, 100 * P + 10 * l + i) for i in range(P)]
+    preps = [dbf_ops.mdbf_prepare_path(_t(p["A_sign_packed"], dev), p["A_shape"], _t(p["B_sign_packed"], dev),
+                                       p["B_shape"], _t(p["A_amp"], dev), _t(p["B_amp"], dev),
+                                       _t(p["Q_U_amp"], dev), _t(p["Q_V_amp"], dev)) for p in paths]
+    x = torch.randn(m_rows, m, generator=torch.Generator().manual_seed(3)).half()
+    y = dbf_ops.mdbf_forward(x.to(dev), preps).float().cpu().numpy()
+    ref = od.mdbf_forward(x.numpy(), paths)
+    assert _rel(y, ref) <= 1e-2, _rel(y, ref)
