@@ -184,7 +184,8 @@ def main():
     ap.add_argument("--m", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every box in this build has a single MI355X and the "
@@ -194,9 +195,24 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
+        return
     r = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev)
     dom = max(r["kernels"], key=lambda k: k["us"])
     value = r["step_bytes"] / r["wall_s"] / 1e9
+    kname = f"k_gemv {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b"
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("kernels", {}).get(kname)
     out = {
         "metric": "M=1 dequant-GEMV HBM GB/s (%peak); M=2048 dequant-GEMM TFLOP/s (%MFMA peak)",
         "value": round(value, 1),
@@ -215,9 +231,9 @@ def main():
                    "M": args.m, "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
                    "weight_copies_rotated": r["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": f"k_gemv {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b",
-                     "avg_us": round(dom["us"], 2)},
+                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": dom["bytes"], "kernel": kname, "avg_us": round(dom["us"], 2),
+                     "traffic_source": "profiles/traffic.json (rocprofv3 --pmc, copy-calibrated)"},
         "per_kernel": [{k: (round(v, 2) if isinstance(v, float) else v) for k, v in kk.items()}
                        for kk in r["kernels"]],
     }
