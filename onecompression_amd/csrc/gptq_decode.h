@@ -89,3 +89,38 @@ __device__ __forceinline__ void decode_kblock(const uint32_t* w, int kbl, oc_u4 
     for (int t = 0; t < 4; ++t) b[t] = oc_u4{pr[4 * t], pr[4 * t + 1], pr[4 * t + 2], pr[4 * t + 3]};
   }
 }
+
+// Decode only MFMA step t (pairs 4t .. 4t+3) of k-block 0 of w.
+template <int BITS, bool BF16>
+__device__ __forceinline__ oc_u4 decode_step(const uint32_t* w, int t, uint32_t msk, uint32_t mag) {
+  if constexpr (BITS == 4) {
+    const uint32_t W = w[t];
+    return oc_u4{and_or(W, msk, mag), and_or(W >> 4, msk, mag), and_or(W >> 8, msk, mag),
+                 and_or(W >> 12, msk, mag)};
+  } else if constexpr (BITS == 8) {
+    const uint32_t W0 = w[2 * t], W1 = w[2 * t + 1];
+    if constexpr (BF16) {
+      return oc_u4{bf16_byte_pair<0>(W0), bf16_byte_pair<1>(W0), bf16_byte_pair<0>(W1), bf16_byte_pair<1>(W1)};
+    } else {
+      return oc_u4{and_or(W0, msk, mag), and_or(W0 >> 8, msk, mag), and_or(W1, msk, mag),
+                   and_or(W1 >> 8, msk, mag)};
+    }
+  } else if constexpr (BITS == 2) {
+    const uint32_t W = w[t >> 1];
+    const int s = 8 * (t & 1);
+    return oc_u4{and_or(W >> s, msk, mag), and_or(W >> (s + 2), msk, mag), and_or(W >> (s + 4), msk, mag),
+                 and_or(W >> (s + 6), msk, mag)};
+  } else {  // BITS == 3
+    uint32_t pr[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int P = 4 * t + p;
+      if (P < 15) {
+        pr[p] = and_or(w[P / 5] >> (3 * (P % 5)), msk, mag);
+      } else {
+        pr[p] = and_or(w[2] >> 13, 0x00040004u, and_or(w[1] >> 14, 0x00020002u, and_or(w[0] >> 15, 0x00010001u, mag)));
+      }
+    }
+    return oc_u4{pr[0], pr[1], pr[2], pr[3]};
+  }
+}

@@ -324,6 +324,222 @@ __global__ void k_splitk_reduce(const float* __restrict__ partial, int S, int M,
   y[(size_t)m * N + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
 }
 
+// ---------------------------------------------------------------------------
+// Large M: fused dequant-GEMM.  A workgroup (4 waves) computes a 256 x 256
+// tile of y; wave w owns the 64 columns (4 n-tiles) 64w..64w+63 for all 256
+// rows.  Per 128-deep k-block:
+//   - the 256 x 128 x-tile is double-buffered in LDS (64 KiB per stage, rows
+//     padded by 16 B), loaded one k-block ahead;
+//   - each wave loads the packed codes of its own 4 n-tiles one k-block ahead
+//     straight into registers (no other wave needs them), decodes them and
+//     dequantises them exactly, W = RNE(s * (q - z)), so the product equals x
+//     times OneComp's dequantised weight with fp32 accumulation;
+//   - 16 m-tiles x 4 n-tiles x 4 steps of v_mfma_f32_16x16x32.
+// Workgroups are mapped so that the ones resident on one XCD share an
+// M-block: its x rows stay in that XCD's L2 while the packed weights stream.
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+  const uint16_t* x;
+  const uint8_t* w;
+  const uint32_t* meta;
+  const uint16_t* bias;
+  uint16_t* y;
+  int M, K, N, N_pad, NT_total, NU, G, gs, gshift, NKB, MB, NB;
+};
+
+constexpr int kGemmBM = 256, kGemmBN = 256, kGemmXS = 136;  // x row stride in halfs (128 + 8)
+
+template <int BITS>
+struct KbWords {
+  static constexpr int n = BITS == 2 ? 2 : (BITS == 3 ? 3 : (BITS == 4 ? 4 : 8));
+};
+
+// Packed words of k-block kb of n-tile nt for this lane (n-tile layout of oc_common.h).
+template <int BITS>
+__device__ __forceinline__ void load_kb_words(const uint8_t* __restrict__ w, int NU, int nt, int kb, int lane,
+                                              uint32_t (&out)[KbWords<BITS>::n]) {
+  using GG = Geo<BITS>;
+  const int u = kb / GG::U, kbl = kb % GG::U;
+  const uint8_t* base = w + ((size_t)(nt * NU + u) * GG::P) * 1024 + lane * 16;
+  if constexpr (BITS == 4) {
+    const oc_u4 v = __builtin_nontemporal_load((const oc_u4*)base);
+    out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+  } else if constexpr (BITS == 8) {
+    const oc_u4 v0 = __builtin_nontemporal_load((const oc_u4*)base);
+    const oc_u4 v1 = __builtin_nontemporal_load((const oc_u4*)(base + 1024));
+    out[0] = v0[0]; out[1] = v0[1]; out[2] = v0[2]; out[3] = v0[3];
+    out[4] = v1[0]; out[5] = v1[1]; out[6] = v1[2]; out[7] = v1[3];
+  } else if constexpr (BITS == 2) {
+    const uint32_t* p = (const uint32_t*)base + 2 * kbl;
+    out[0] = __builtin_nontemporal_load(p);
+    out[1] = __builtin_nontemporal_load(p + 1);
+  } else {  // 3 words of k-block kbl inside the 12-word payload (3 parts of 4 words)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int wi = 3 * kbl + q;
+      out[q] = __builtin_nontemporal_load((const uint32_t*)(base + (wi >> 2) * 1024) + (wi & 3));
+    }
+  }
+}
+
+// Exact dequantisation of one (off + q) pair word: RNE(s * (q - z)) for both halves.
+template <bool BF16>
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t pr, uint32_t ozz_h2, uint32_t s_h2, float s_f, float c_f) {
+  if constexpr (BF16) {
+    const float lo = fmaf(__builtin_bit_cast(float, pr << 16), s_f, c_f);
+    const float hi = fmaf(__builtin_bit_cast(float, pr & 0xFFFF0000u), s_f, c_f);
+    return (uint32_t)oc_f2bf(lo) | ((uint32_t)oc_f2bf(hi) << 16);
+  } else {
+    const oc_half2 d = __builtin_bit_cast(oc_half2, pr) - __builtin_bit_cast(oc_half2, ozz_h2);
+    return __builtin_bit_cast(uint32_t, d * __builtin_bit_cast(oc_half2, s_h2));
+  }
+}
+
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
+  constexpr int NWB = KbWords<BITS>::n;
+  constexpr float OFF = dec_offset<BITS, BF16>();
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, kq = lane >> 4;
+  // XCD-aware tile order: consecutive workgroups go to consecutive XCDs.
+  const int L = blockIdx.x;
+  int mb, nb;
+  if ((a.MB % 8) == 0) {
+    const int xcd = L & 7, j = L >> 3;
+    mb = (j / a.NB) * 8 + xcd;
+    nb = j % a.NB;
+  } else {
+    mb = L / a.NB;
+    nb = L % a.NB;
+  }
+  const int m0 = mb * kGemmBM;
+  int nt[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) nt[j] = min((nb * kGemmBN) / 16 + wave * 4 + j, a.NT_total - 1);
+  const uint32_t msk = oc_opaque(Geo<BITS>::MASK), mag = oc_opaque(dec_magic<BF16>());
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint16_t* xs0 = (uint16_t*)smem;
+  uint16_t* xs1 = xs0 + kGemmBM * kGemmXS;
+
+  // x tile loads: 256 rows x 16 chunks of 8 halfs, 16 chunks per thread
+  oc_u4 xr[16];
+  auto load_x = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+      const int m = m0 + row, k = kb * 128 + ch * 8;
+      xr[i] = (m < a.M && k < a.K) ? *(const oc_u4*)(a.x + (size_t)m * a.K + k) : oc_u4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_x = [&](uint16_t* xs) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+      *(oc_u4*)(xs + row * kGemmXS + ch * 8) = xr[i];
+    }
+  };
+  uint32_t wcur[4][NWB], wnxt[4][NWB];
+  uint32_t mcur[4][4], mnxt[4][4];
+  auto load_w = [&](int kb, uint32_t (&wbuf)[4][NWB], uint32_t (&mbuf)[4][4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      load_kb_words<BITS>(a.w, a.NU, nt[j], kb, lane, wbuf[j]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int k = kb * 128 + 32 * t;
+        const int g = min(a.gshift >= 0 ? (k >> a.gshift) : k / a.gs, a.G - 1);
+        mbuf[j][t] = a.meta[(size_t)g * a.N_pad + nt[j] * 16 + col];
+      }
+    }
+  };
+
+  oc_f4 acc[16][4];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = oc_f4{0.f, 0.f, 0.f, 0.f};
+
+  load_x(0);
+  load_w(0, wcur, mcur);
+  store_x(xs0);
+  __syncthreads();
+  const uint16_t* xcur = xs0;
+  uint16_t* xnext = xs1;
+  for (int kb = 0; kb < a.NKB; ++kb) {
+    const bool more = kb + 1 < a.NKB;
+    if (more) {
+      load_x(kb + 1);
+      load_w(kb + 1, wnxt, mnxt);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      // one MFMA step: dequantise the 4 n-tiles' B operands, then 16 m-tiles
+      oc_u4 bw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const oc_u4 bq = decode_step<BITS, BF16>(wcur[j], t, msk, mag);
+        const uint32_t md = mcur[j][t];
+        const uint16_t sh = (uint16_t)(md & 0xFFFFu);
+        const float sf = oc_h2f(sh);
+        const float zoff = OFF + (float)(md >> 16);
+        uint32_t s_h2 = 0, ozz_h2 = 0;
+        float cf = 0.f;
+        if constexpr (BF16) {
+          cf = -sf * zoff;  // exact: 11-bit scale times a <= 9-bit integer
+        } else {
+          s_h2 = (uint32_t)sh | ((uint32_t)sh << 16);
+          const uint16_t oz = oc_f2h(zoff);
+          ozz_h2 = (uint32_t)oz | ((uint32_t)oz << 16);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) bw[j][p] = dequant_pair<BF16>(bq[p], ozz_h2, s_h2, sf, cf);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int i = 8 * h; i < 8 * h + 8; ++i) {
+          const oc_u4 av = *(const oc_u4*)(xcur + (i * 16 + col) * kGemmXS + 32 * t + 8 * kq);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = oc_mfma16<BF16>(av, bw[j], acc[i][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (more) store_x(xnext);
+    __syncthreads();
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int q = 0; q < NWB; ++q) wcur[j][q] = wnxt[j][q];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) mcur[j][t] = mnxt[j][t];
+      }
+      const uint16_t* tmp = xcur;
+      xcur = xnext;
+      xnext = (uint16_t*)tmp;
+    }
+  }
+
+  // epilogue: lane holds rows 16i + 4kq + r, column 16 nt[j] + col
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = ((nb * kGemmBN) / 16 + wave * 4 + j) * 16 + col;
+    if (n >= a.N) continue;
+    float b = 0.f;
+    if (a.bias) b = BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + i * 16 + 4 * kq + r;
+        if (m < a.M) a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(acc[i][j][r] + b) : oc_f2h(acc[i][j][r] + b);
+      }
+  }
+}
+
 // x_perm[m, p] = x[m, perm[p]] (act-order activations, 16-bit elements).
 __global__ void k_gather(const uint16_t* __restrict__ x, const int32_t* __restrict__ perm, int M, int K,
                          uint16_t* __restrict__ xp) {
@@ -494,6 +710,7 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
     if (p.S > 1) ws += align256((size_t)p.S * M * L.N_pad * 4);
     return ws;
   }
+  if (M >= env_int("OC_GEMM_MIN_M", 128)) return ws;
   const int Mc = M < kSkinnyMaxM ? M : kSkinnyMaxM;
   const SkinnyPlan p = plan_skinny(L, Mc);
   if (p.S > 1) ws += align256((size_t)p.S * Mc * L.N_pad * 4);
@@ -550,6 +767,41 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     const int rc = bf16 ? dispatch_gemv_bits<true>(bits, p, a, st) : dispatch_gemv_bits<false>(bits, p, a, st);
     if (rc || p.S == 1) return rc;
     return launch_reduce(bf16, a.partial, p.S, M, N, L.N_pad, bias, y, st);
+  }
+  if (M >= env_int("OC_GEMM_MIN_M", 128)) {
+    GemmArgs g;
+    g.x = xa;
+    g.w = (const uint8_t*)packed;
+    g.meta = meta;
+    g.bias = (const uint16_t*)bias;
+    g.y = (uint16_t*)y;
+    g.M = M;
+    g.K = K;
+    g.N = N;
+    g.N_pad = L.N_pad;
+    g.NT_total = L.NT;
+    g.NU = L.NU;
+    g.G = G;
+    g.gs = gs;
+    g.gshift = log2_exact(gs);
+    g.NKB = L.K_pad / 128;
+    g.MB = (M + kGemmBM - 1) / kGemmBM;
+    g.NB = (L.N_pad + kGemmBN - 1) / kGemmBN;
+    const size_t lds = (size_t)2 * kGemmBM * kGemmXS * 2;
+    const dim3 grid(g.MB * g.NB);
+    switch (bits) {
+#define OC_GM(B_)                                                                                  \
+  case B_:                                                                                         \
+    if (bf16)                                                                                      \
+      hipLaunchKernelGGL((k_gemm<B_, true>), grid, dim3(256), lds, st, g);                         \
+    else                                                                                           \
+      hipLaunchKernelGGL((k_gemm<B_, false>), grid, dim3(256), lds, st, g);                        \
+    break;
+      OC_GM(2) OC_GM(3) OC_GM(4) OC_GM(8)
+#undef OC_GM
+    }
+    OC_HIP(hipGetLastError());
+    return 0;
   }
   // Rows are processed in chunks of at most 64 by the skinny kernel.
   for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {

@@ -163,3 +163,22 @@ def test_gemv_plan_variants(dev, monkeypatch, bits, w, nt):
     c = _case(4096, 256 if bits != 3 else 320, bits, seed=60 + bits)
     for m in (1, 7):
         _gemm_check(dev, c, m, "fp16", bias=m == 7)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m,k,n,gs,act,dtype", [
+    (128, 1024, 256, 128, False, "fp16"),
+    (300, 1056, 272, 32, False, "bf16"),     # ragged M, K not a multiple of the k-unit, N not of 256
+    (256, 2048, 512, 128, True, "fp16"),     # act-order
+    (129, 512, 528, -1, False, "bf16"),      # one group, bias below
+])
+def test_gemm_large_m(dev, bits, m, k, n, gs, act, dtype):
+    if bits == 3 and n % 32:
+        n = (n + 31) // 32 * 32
+    c = _case(k, n, bits, gs, act, seed=bits * 31 + m)
+    _gemm_check(dev, c, m, dtype, bias=(m == 129))
+
+
+def test_gemm_large_m_config4_shape(dev):
+    c = synth.gptq_case("o", 5120, 5120, 4, 128, False, seed=3)
+    _gemm_check(dev, c, 512, "bf16")
