@@ -325,16 +325,18 @@ __global__ void k_splitk_reduce(const float* __restrict__ partial, int S, int M,
 }
 
 // ---------------------------------------------------------------------------
-// Large M: fused dequant-GEMM.  A workgroup (4 waves) computes a 256 x 256
-// tile of y; wave w owns the 64 columns (4 n-tiles) 64w..64w+63 for all 256
-// rows.  Per 128-deep k-block:
-//   - the 256 x 128 x-tile is double-buffered in LDS (64 KiB per stage, rows
+// Large M: fused dequant-GEMM.  A workgroup (8 waves, 2 per SIMD) computes a
+// 128 x 512 tile of y; wave w owns the 64 columns (4 n-tiles) 64w..64w+63 for
+// all 128 rows, so no two waves dequantise the same weights.  Per 128-deep
+// k-block:
+//   - the 128 x 128 x-tile is double-buffered in LDS (32 KiB per stage, rows
 //     padded by 16 B), loaded one k-block ahead;
-//   - each wave loads the packed codes of its own 4 n-tiles one k-block ahead
-//     straight into registers (no other wave needs them), decodes them and
-//     dequantises them exactly, W = RNE(s * (q - z)), so the product equals x
-//     times OneComp's dequantised weight with fp32 accumulation;
-//   - 16 m-tiles x 4 n-tiles x 4 steps of v_mfma_f32_16x16x32.
+//   - each wave loads the packed codes (and scale/zero words) of its own 4
+//     n-tiles one k-block ahead straight into registers, then per MFMA step
+//     decodes and dequantises them exactly, W = RNE(s * (q - z)), so the
+//     product is x times OneComp's dequantised weight, fp32 accumulated;
+//   - 8 m-tiles x 4 n-tiles x 4 steps of v_mfma_f32_16x16x32.
+// Two waves per SIMD let one wave's dequantisation overlap the other's MFMAs.
 // Workgroups are mapped so that the ones resident on one XCD share an
 // M-block: its x rows stay in that XCD's L2 while the packed weights stream.
 // ---------------------------------------------------------------------------
@@ -347,7 +349,7 @@ struct GemmArgs {
   int M, K, N, N_pad, NT_total, NU, G, gs, gshift, NKB, MB, NB;
 };
 
-constexpr int kGemmBM = 256, kGemmBN = 256, kGemmXS = 136;  // x row stride in halfs (128 + 8)
+constexpr int kGemmBM = 128, kGemmBN = 512, kGemmXS = 136;  // x row stride in halfs (128 + 8)
 
 template <int BITS>
 struct KbWords {
@@ -395,9 +397,34 @@ __device__ __forceinline__ uint32_t dequant_pair(uint32_t pr, uint32_t ozz_h2, u
   }
 }
 
-template <int BITS, bool BF16>
-__global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
+__device__ __forceinline__ uint32_t bf16_pair_f32(float lo, float hi) {
+  return (uint32_t)oc_f2bf(lo) | ((uint32_t)oc_f2bf(hi) << 16);
+}
+
+// bf16 B operand of step t for 4-bit codes: bytes of (w & 0x0F0F0F0F) hold the
+// codes of nibbles 0,2,4,6 = k {0,4,1,5}; of ((w >> 4) & ..) nibbles 1,3,5,7 =
+// k {2,6,3,7}; v_cvt_f32_ubyte turns each into an exact float.
+__device__ __forceinline__ oc_u4 dequant_step_b4_bf16(uint32_t W, float s, float c) {
+  const uint32_t lo = W & 0x0F0F0F0Fu, hi = (W >> 4) & 0x0F0F0F0Fu;
+  const float k0 = fmaf((float)(lo & 0xFFu), s, c), k4 = fmaf((float)((lo >> 8) & 0xFFu), s, c);
+  const float k1 = fmaf((float)((lo >> 16) & 0xFFu), s, c), k5 = fmaf((float)(lo >> 24), s, c);
+  const float k2 = fmaf((float)(hi & 0xFFu), s, c), k6 = fmaf((float)((hi >> 8) & 0xFFu), s, c);
+  const float k3 = fmaf((float)((hi >> 16) & 0xFFu), s, c), k7 = fmaf((float)(hi >> 24), s, c);
+  return oc_u4{bf16_pair_f32(k0, k1), bf16_pair_f32(k2, k3), bf16_pair_f32(k4, k5), bf16_pair_f32(k6, k7)};
+}
+
+// bf16 B operand of step t for 8-bit codes: word 2t holds k {0,2,1,3}, word
+// 2t+1 holds k {4,6,5,7} (bytes b and b+2 form the pair of slot b).
+__device__ __forceinline__ oc_u4 dequant_step_b8_bf16(uint32_t W0, uint32_t W1, float s, float c) {
+  auto f = [&](uint32_t W, int b) { return fmaf((float)((W >> (8 * b)) & 0xFFu), s, c); };
+  return oc_u4{bf16_pair_f32(f(W0, 0), f(W0, 2)), bf16_pair_f32(f(W0, 1), f(W0, 3)),
+               bf16_pair_f32(f(W1, 0), f(W1, 2)), bf16_pair_f32(f(W1, 1), f(W1, 3))};
+}
+
+template <int BITS, int CS, bool BF16>
+__global__ __launch_bounds__(512, 1) void k_gemm(const GemmArgs a) {
   constexpr int NWB = KbWords<BITS>::n;
+  constexpr int SPK = 4 / CS;  // scale/zero words per n-tile per k-block
   constexpr float OFF = dec_offset<BITS, BF16>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -414,50 +441,51 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     nb = L % a.NB;
   }
   const int m0 = mb * kGemmBM;
+  const int nt0 = (nb * kGemmBN) / 16 + wave * 4;
   int nt[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) nt[j] = min((nb * kGemmBN) / 16 + wave * 4 + j, a.NT_total - 1);
+  for (int j = 0; j < 4; ++j) nt[j] = min(nt0 + j, a.NT_total - 1);
   const uint32_t msk = oc_opaque(Geo<BITS>::MASK), mag = oc_opaque(dec_magic<BF16>());
 
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* xs0 = (uint16_t*)smem;
   uint16_t* xs1 = xs0 + kGemmBM * kGemmXS;
 
-  // x tile loads: 256 rows x 16 chunks of 8 halfs, 16 chunks per thread
-  oc_u4 xr[16];
+  // x tile: 128 rows x 16 chunks of 8 halfs, 4 chunks per thread
+  oc_u4 xr[4];
   auto load_x = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 512 * i, row = c >> 4, ch = c & 15;
       const int m = m0 + row, k = kb * 128 + ch * 8;
       xr[i] = (m < a.M && k < a.K) ? *(const oc_u4*)(a.x + (size_t)m * a.K + k) : oc_u4{0u, 0u, 0u, 0u};
     }
   };
   auto store_x = [&](uint16_t* xs) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 512 * i, row = c >> 4, ch = c & 15;
       *(oc_u4*)(xs + row * kGemmXS + ch * 8) = xr[i];
     }
   };
   uint32_t wcur[4][NWB], wnxt[4][NWB];
-  uint32_t mcur[4][4], mnxt[4][4];
-  auto load_w = [&](int kb, uint32_t (&wbuf)[4][NWB], uint32_t (&mbuf)[4][4]) {
+  uint32_t mcur[4][SPK], mnxt[4][SPK];
+  auto load_w = [&](int kb, uint32_t (&wbuf)[4][NWB], uint32_t (&mbuf)[4][SPK]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       load_kb_words<BITS>(a.w, a.NU, nt[j], kb, lane, wbuf[j]);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int k = kb * 128 + 32 * t;
+      for (int q = 0; q < SPK; ++q) {
+        const int k = kb * 128 + 32 * CS * q;
         const int g = min(a.gshift >= 0 ? (k >> a.gshift) : k / a.gs, a.G - 1);
-        mbuf[j][t] = a.meta[(size_t)g * a.N_pad + nt[j] * 16 + col];
+        mbuf[j][q] = a.meta[(size_t)g * a.N_pad + nt[j] * 16 + col];
       }
     }
   };
 
-  oc_f4 acc[16][4];
+  oc_f4 acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = oc_f4{0.f, 0.f, 0.f, 0.f};
 
@@ -475,37 +503,40 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      // one MFMA step: dequantise the 4 n-tiles' B operands, then 16 m-tiles
+      // one MFMA step: the 4 n-tiles' B operands, then 8 m-tiles
       oc_u4 bw[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const oc_u4 bq = decode_step<BITS, BF16>(wcur[j], t, msk, mag);
-        const uint32_t md = mcur[j][t];
+        const uint32_t md = mcur[j][t / CS];
         const uint16_t sh = (uint16_t)(md & 0xFFFFu);
         const float sf = oc_h2f(sh);
         const float zoff = OFF + (float)(md >> 16);
-        uint32_t s_h2 = 0, ozz_h2 = 0;
-        float cf = 0.f;
-        if constexpr (BF16) {
-          cf = -sf * zoff;  // exact: 11-bit scale times a <= 9-bit integer
+        if constexpr (BF16 && BITS == 4) {
+          bw[j] = dequant_step_b4_bf16(wcur[j][t], sf, -sf * (float)(md >> 16));
+        } else if constexpr (BF16 && BITS == 8) {
+          bw[j] = dequant_step_b8_bf16(wcur[j][2 * t], wcur[j][2 * t + 1], sf, -sf * (float)(md >> 16));
         } else {
-          s_h2 = (uint32_t)sh | ((uint32_t)sh << 16);
-          const uint16_t oz = oc_f2h(zoff);
-          ozz_h2 = (uint32_t)oz | ((uint32_t)oz << 16);
-        }
+          const oc_u4 bq = decode_step<BITS, BF16>(wcur[j], t, msk, mag);
+          uint32_t s_h2 = 0, ozz_h2 = 0;
+          float cf = 0.f;
+          if constexpr (BF16) {
+            cf = -sf * zoff;  // exact: 11-bit scale times a <= 9-bit integer
+          } else {
+            s_h2 = (uint32_t)sh | ((uint32_t)sh << 16);
+            const uint16_t oz = oc_f2h(zoff);
+            ozz_h2 = (uint32_t)oz | ((uint32_t)oz << 16);
+          }
 #pragma unroll
-        for (int p = 0; p < 4; ++p) bw[j][p] = dequant_pair<BF16>(bq[p], ozz_h2, s_h2, sf, cf);
+          for (int p = 0; p < 4; ++p) bw[j][p] = dequant_pair<BF16>(bq[p], ozz_h2, s_h2, sf, cf);
+        }
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int i = 0; i < 8; ++i) {
+        const oc_u4 av = *(const oc_u4*)(xcur + (i * 16 + col) * kGemmXS + 32 * t + 8 * kq);
 #pragma unroll
-        for (int i = 8 * h; i < 8 * h + 8; ++i) {
-          const oc_u4 av = *(const oc_u4*)(xcur + (i * 16 + col) * kGemmXS + 32 * t + 8 * kq);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = oc_mfma16<BF16>(av, bw[j], acc[i][j]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < 4; ++j) acc[i][j] = oc_mfma16<BF16>(av, bw[j], acc[i][j]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (more) store_x(xnext);
     __syncthreads();
@@ -515,7 +546,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 #pragma unroll
         for (int q = 0; q < NWB; ++q) wcur[j][q] = wnxt[j][q];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) mcur[j][t] = mnxt[j][t];
+        for (int q = 0; q < SPK; ++q) mcur[j][q] = mnxt[j][q];
       }
       const uint16_t* tmp = xcur;
       xcur = xnext;
@@ -523,15 +554,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     }
   }
 
-  // epilogue: lane holds rows 16i + 4kq + r, column 16 nt[j] + col
+  // epilogue: lane holds rows 16i + 4kq + r of column 16 nt + col
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int n = ((nb * kGemmBN) / 16 + wave * 4 + j) * 16 + col;
+    const int n = (nt0 + j) * 16 + col;
     if (n >= a.N) continue;
     float b = 0.f;
     if (a.bias) b = BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + i * 16 + 4 * kq + r;
@@ -789,13 +820,17 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     g.NB = (L.N_pad + kGemmBN - 1) / kGemmBN;
     const size_t lds = (size_t)2 * kGemmBM * kGemmXS * 2;
     const dim3 grid(g.MB * g.NB);
+    const bool cs4 = (gs % 128) == 0;
     switch (bits) {
 #define OC_GM(B_)                                                                                  \
   case B_:                                                                                         \
-    if (bf16)                                                                                      \
-      hipLaunchKernelGGL((k_gemm<B_, true>), grid, dim3(256), lds, st, g);                         \
-    else                                                                                           \
-      hipLaunchKernelGGL((k_gemm<B_, false>), grid, dim3(256), lds, st, g);                        \
+    if (bf16) {                                                                                    \
+      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, true>), grid, dim3(512), lds, st, g);             \
+      else hipLaunchKernelGGL((k_gemm<B_, 1, true>), grid, dim3(512), lds, st, g);                 \
+    } else {                                                                                       \
+      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, false>), grid, dim3(512), lds, st, g);            \
+      else hipLaunchKernelGGL((k_gemm<B_, 1, false>), grid, dim3(512), lds, st, g);                \
+    }                                                                                              \
     break;
       OC_GM(2) OC_GM(3) OC_GM(4) OC_GM(8)
 #undef OC_GM
