@@ -15,7 +15,7 @@
 // which on gfx950 write back and invalidate the whole per-XCD L2: measured
 // ~50 us per call.)
 //
-// Large M: see k_gemm_lds below (dequantised tiles staged in LDS).
+// Large M: k_gemm below (x tiles staged in LDS, weights dequantised in registers).
 #include <stdlib.h>
 
 #include "gptq_decode.h"
@@ -324,22 +324,6 @@ __global__ void k_splitk_reduce(const float* __restrict__ partial, int S, int M,
   y[(size_t)m * N + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
 }
 
-// ---------------------------------------------------------------------------
-// Large M: fused dequant-GEMM.  A workgroup (8 waves, 2 per SIMD) computes a
-// 128 x 512 tile of y; wave w owns the 64 columns (4 n-tiles) 64w..64w+63 for
-// all 128 rows, so no two waves dequantise the same weights.  Per 128-deep
-// k-block:
-//   - the 128 x 128 x-tile is double-buffered in LDS (32 KiB per stage, rows
-//     padded by 16 B), loaded one k-block ahead;
-//   - each wave loads the packed codes (and scale/zero words) of its own 4
-//     n-tiles one k-block ahead straight into registers, then per MFMA step
-//     decodes and dequantises them exactly, W = RNE(s * (q - z)), so the
-//     product is x times OneComp's dequantised weight, fp32 accumulated;
-//   - 8 m-tiles x 4 n-tiles x 4 steps of v_mfma_f32_16x16x32.
-// Two waves per SIMD let one wave's dequantisation overlap the other's MFMAs.
-// Workgroups are mapped so that the ones resident on one XCD share an
-// M-block: its x rows stay in that XCD's L2 while the packed weights stream.
-// ---------------------------------------------------------------------------
 struct GemmArgs {
   const uint16_t* x;
   const uint8_t* w;
@@ -349,87 +333,120 @@ struct GemmArgs {
   int M, K, N, N_pad, NT_total, NU, G, gs, gshift, NKB, MB, NB;
 };
 
-constexpr int kGemmBM = 128, kGemmBN = 512, kGemmXS = 136;  // x row stride in halfs (128 + 8)
-
+// Packed words of one k-block per lane and chunk (lane-chunk layout of oc_common.h).
 template <int BITS>
 struct KbWords {
   static constexpr int n = BITS == 2 ? 2 : (BITS == 3 ? 3 : (BITS == 4 ? 4 : 8));
 };
 
-// Packed words of k-block kb of n-tile nt for this lane (n-tile layout of oc_common.h).
-template <int BITS>
-__device__ __forceinline__ void load_kb_words(const uint8_t* __restrict__ w, int NU, int nt, int kb, int lane,
-                                              uint32_t (&out)[KbWords<BITS>::n]) {
-  using GG = Geo<BITS>;
-  const int u = kb / GG::U, kbl = kb % GG::U;
-  const uint8_t* base = w + ((size_t)(nt * NU + u) * GG::P) * 1024 + lane * 16;
-  if constexpr (BITS == 4) {
-    const oc_u4 v = __builtin_nontemporal_load((const oc_u4*)base);
-    out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
-  } else if constexpr (BITS == 8) {
-    const oc_u4 v0 = __builtin_nontemporal_load((const oc_u4*)base);
-    const oc_u4 v1 = __builtin_nontemporal_load((const oc_u4*)(base + 1024));
-    out[0] = v0[0]; out[1] = v0[1]; out[2] = v0[2]; out[3] = v0[3];
-    out[4] = v1[0]; out[5] = v1[1]; out[6] = v1[2]; out[7] = v1[3];
-  } else if constexpr (BITS == 2) {
-    const uint32_t* p = (const uint32_t*)base + 2 * kbl;
-    out[0] = __builtin_nontemporal_load(p);
-    out[1] = __builtin_nontemporal_load(p + 1);
-  } else {  // 3 words of k-block kbl inside the 12-word payload (3 parts of 4 words)
-#pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const int wi = 3 * kbl + q;
-      out[q] = __builtin_nontemporal_load((const uint32_t*)(base + (wi >> 2) * 1024) + (wi & 3));
-    }
-  }
-}
+typedef float oc_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 oc_bf2 __attribute__((ext_vector_type(2)));
 
-// Exact dequantisation of one (off + q) pair word: RNE(s * (q - z)) for both halves.
-template <bool BF16>
-__device__ __forceinline__ uint32_t dequant_pair(uint32_t pr, uint32_t ozz_h2, uint32_t s_h2, float s_f, float c_f) {
-  if constexpr (BF16) {
-    const float lo = fmaf(__builtin_bit_cast(float, pr << 16), s_f, c_f);
-    const float hi = fmaf(__builtin_bit_cast(float, pr & 0xFFFF0000u), s_f, c_f);
-    return (uint32_t)oc_f2bf(lo) | ((uint32_t)oc_f2bf(hi) << 16);
-  } else {
-    const oc_half2 d = __builtin_bit_cast(oc_half2, pr) - __builtin_bit_cast(oc_half2, ozz_h2);
-    return __builtin_bit_cast(uint32_t, d * __builtin_bit_cast(oc_half2, s_h2));
-  }
-}
-
+// Two fp32 values rounded (RNE) to one bf16 pair word: v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t bf16_pair_f32(float lo, float hi) {
-  return (uint32_t)oc_f2bf(lo) | ((uint32_t)oc_f2bf(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(oc_f2{lo, hi}, oc_bf2));
 }
 
-// bf16 B operand of step t for 4-bit codes: bytes of (w & 0x0F0F0F0F) hold the
-// codes of nibbles 0,2,4,6 = k {0,4,1,5}; of ((w >> 4) & ..) nibbles 1,3,5,7 =
-// k {2,6,3,7}; v_cvt_f32_ubyte turns each into an exact float.
-__device__ __forceinline__ oc_u4 dequant_step_b4_bf16(uint32_t W, float s, float c) {
-  const uint32_t lo = W & 0x0F0F0F0Fu, hi = (W >> 4) & 0x0F0F0F0Fu;
-  const float k0 = fmaf((float)(lo & 0xFFu), s, c), k4 = fmaf((float)((lo >> 8) & 0xFFu), s, c);
-  const float k1 = fmaf((float)((lo >> 16) & 0xFFu), s, c), k5 = fmaf((float)(lo >> 24), s, c);
-  const float k2 = fmaf((float)(hi & 0xFFu), s, c), k6 = fmaf((float)((hi >> 8) & 0xFFu), s, c);
-  const float k3 = fmaf((float)((hi >> 16) & 0xFFu), s, c), k7 = fmaf((float)(hi >> 24), s, c);
-  return oc_u4{bf16_pair_f32(k0, k1), bf16_pair_f32(k2, k3), bf16_pair_f32(k4, k5), bf16_pair_f32(k6, k7)};
+// ---------------------------------------------------------------------------
+// Large M: fused dequant-GEMM with 32x32x16 MFMAs.  One wave per SIMD (4 waves, 256 threads)
+// computes a 256 x 256 tile; wave w owns columns [64w, 64w + 64) over all 256
+// rows, so every dequantised B fragment feeds 8 MFMAs.  The accumulators
+// (8 x 2 tiles of 32 x 32 fp32 = 256 registers per lane) live in AGPRs.
+//
+// x tiles (256 rows x 128 k, 64 KB) go from HBM straight into LDS with
+// buffer_load ... lds (no VGPR staging); 16-B chunk c of row r is stored at
+// chunk position c ^ (r % 16) so that the A-fragment reads of 16 consecutive
+// rows hit 16 distinct bank groups.  Rows >= M and chunks at k >= K read as
+// zero through the buffer's range check.  Two LDS buffers alternate per
+// k-block.
+//
+// B operands: the 32 columns of an MFMA are two 16-column chunks of the
+// packed layout.  Lane l needs column l % 32 and the k-slice 8(l/32) of each
+// 16-deep step; in chunk terms that is chunk-lane (l % 16) + 16 q with
+// q = 2(s % 2) + l/32 for step s, so each lane loads two chunk-lanes per
+// n32-tile and decodes exactly as the 16-column kernels do.  Codes decode to
+// fp16 (1024 + q); fp16 output uses packed half subtract/multiply, bf16
+// output forms s * (1024 + q) - s * (1024 + z) with one fma per value on an
+// fp16 operand (v_fma_mix), exact in fp32, then rounds once to bf16.
+// ---------------------------------------------------------------------------
+constexpr int kGemmBM = 256, kGemmBN = 256;
+constexpr size_t kGemmXBuf = (size_t)kGemmBM * 256;  // bytes of one x buffer (128 k of bf16 per row)
+
+typedef __attribute__((address_space(3))) void* oc_lds_ptr;
+
+template <bool BF16>
+struct GemmDeq {
+  // fp16: pair (1024+z) and pair s; bf16: s and -s * (1024 + z) as fp32
+  uint32_t a, b;
+};
+
+template <bool BF16>
+__device__ __forceinline__ GemmDeq<BF16> gemm_deq(uint32_t md) {
+  GemmDeq<BF16> d;
+  const uint16_t sh = (uint16_t)(md & 0xFFFFu);
+  const float zoff = 1024.f + (float)(md >> 16);
+  if constexpr (BF16) {
+    const float sf = oc_h2f(sh);
+    d.a = __builtin_bit_cast(uint32_t, sf);
+    d.b = __builtin_bit_cast(uint32_t, -sf * zoff);  // exact: 11-bit scale times an 11-bit integer
+  } else {
+    const uint16_t oz = oc_f2h(zoff);
+    d.a = (uint32_t)oz | ((uint32_t)oz << 16);
+    d.b = (uint32_t)sh | ((uint32_t)sh << 16);
+  }
+  return d;
 }
 
-// bf16 B operand of step t for 8-bit codes: word 2t holds k {0,2,1,3}, word
-// 2t+1 holds k {4,6,5,7} (bytes b and b+2 form the pair of slot b).
-__device__ __forceinline__ oc_u4 dequant_step_b8_bf16(uint32_t W0, uint32_t W1, float s, float c) {
-  auto f = [&](uint32_t W, int b) { return fmaf((float)((W >> (8 * b)) & 0xFFu), s, c); };
-  return oc_u4{bf16_pair_f32(f(W0, 0), f(W0, 2)), bf16_pair_f32(f(W0, 1), f(W0, 3)),
-               bf16_pair_f32(f(W1, 0), f(W1, 2)), bf16_pair_f32(f(W1, 1), f(W1, 3))};
+template <bool BF16>
+__device__ __forceinline__ uint32_t gemm_pair(uint32_t pr, GemmDeq<BF16> d) {
+  if constexpr (BF16) {
+    const oc_half2 h = __builtin_bit_cast(oc_half2, pr);
+    const float sf = __builtin_bit_cast(float, d.a), cf = __builtin_bit_cast(float, d.b);
+    return bf16_pair_f32(fmaf((float)h[0], sf, cf), fmaf((float)h[1], sf, cf));
+  } else {
+    const oc_half2 v = (__builtin_bit_cast(oc_half2, pr) - __builtin_bit_cast(oc_half2, d.a)) *
+                       __builtin_bit_cast(oc_half2, d.b);
+    return __builtin_bit_cast(uint32_t, v);
+  }
 }
+
+// Built element by element on purpose: filling the vector in a loop has been
+// miscompiled here (every element took the value of element 0).
+template <bool BF16>
+__device__ __forceinline__ oc_u4 gemm_apply(oc_u4 pr, GemmDeq<BF16> d) {
+  return oc_u4{gemm_pair<BF16>(pr[0], d), gemm_pair<BF16>(pr[1], d), gemm_pair<BF16>(pr[2], d),
+               gemm_pair<BF16>(pr[3], d)};
+}
+
+// Scheduling of one 16-MFMA step: the next step's LDS reads go out first (16
+// MFMAs before their use), then each MFMA is followed by a share of the next
+// step's dequantisation, so the matrix pipe never waits on a burst of VALU.
+__device__ __forceinline__ void gemm_interleave() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the next step's 8 LDS reads first
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Vector-memory instructions of one k-block's weight loads in k_gemm: per
+// n32-tile and chunk-lane half, b4 one 16-B load, b8 two, b2 one 8-B load, b3
+// three 4-B loads; plus one scale/zero word per n32-tile and group segment.
+template <int BITS, int CS>
+struct GemmLoads {
+  static constexpr int per = BITS == 8 ? 2 : (BITS == 3 ? 3 : 1);
+  static constexpr int n = 4 * per + 2 * (4 / CS);
+};
 
 template <int BITS, int CS, bool BF16>
-__global__ __launch_bounds__(512, 1) void k_gemm(const GemmArgs a) {
+__global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   constexpr int NWB = KbWords<BITS>::n;
-  constexpr int SPK = 4 / CS;  // scale/zero words per n-tile per k-block
-  constexpr float OFF = dec_offset<BITS, BF16>();
+  constexpr int SPK = 4 / CS;  // meta words per n32-tile per k-block
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 15, kq = lane >> 4;
-  // XCD-aware tile order: consecutive workgroups go to consecutive XCDs.
+  const int h = lane >> 5, r16 = lane & 15;
   const int L = blockIdx.x;
   int mb, nb;
   if ((a.MB % 8) == 0) {
@@ -441,132 +458,196 @@ __global__ __launch_bounds__(512, 1) void k_gemm(const GemmArgs a) {
     nb = L % a.NB;
   }
   const int m0 = mb * kGemmBM;
-  const int nt0 = (nb * kGemmBN) / 16 + wave * 4;
-  int nt[4];
+  const int n0 = nb * kGemmBN + wave * 64;  // first column of this wave
+  int nt[2], cl[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) nt[j] = min(nt0 + j, a.NT_total - 1);
-  const uint32_t msk = oc_opaque(Geo<BITS>::MASK), mag = oc_opaque(dec_magic<BF16>());
+  for (int T = 0; T < 2; ++T) nt[T] = min(n0 / 16 + 2 * T + ((lane >> 4) & 1), a.NT_total - 1);
+#pragma unroll
+  for (int q2 = 0; q2 < 2; ++q2) cl[q2] = r16 + 16 * (2 * q2 + h);
+  const uint32_t msk = oc_opaque(Geo<BITS>::MASK), mag = oc_opaque(dec_magic<false>());
 
   extern __shared__ __align__(16) uint8_t smem[];
-  uint16_t* xs0 = (uint16_t*)smem;
-  uint16_t* xs1 = xs0 + kGemmBM * kGemmXS;
 
-  // x tile: 128 rows x 16 chunks of 8 halfs, 4 chunks per thread
-  oc_u4 xr[4];
-  auto load_x = [&](int kb) {
+  // x tile loader: wave w, instruction j fills LDS bytes [(16w + j) KB, +1 KB):
+  // row 64w + 4j + lane/16, chunk position lane % 16.
+  const int rows_here = min(a.M - m0, kGemmBM);
+  const int K2 = a.K * 2;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (size_t)m0 * a.K), 0, rows_here * K2, 0x00020000);
+  const int xrow = 64 * wave + (lane >> 4);
+  int xcoff[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 512 * i, row = c >> 4, ch = c & 15;
-      const int m = m0 + row, k = kb * 128 + ch * 8;
-      xr[i] = (m < a.M && k < a.K) ? *(const oc_u4*)(a.x + (size_t)m * a.K + k) : oc_u4{0u, 0u, 0u, 0u};
+  for (int j = 0; j < 4; ++j) xcoff[j] = (r16 ^ ((4 * j + (lane >> 4)) & 15));
+  auto load_x = [&](int kb, int buf) {
+    const bool tail = (kb + 1) * 128 > a.K;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int c = xcoff[j & 3];
+      int off = (xrow + 4 * j) * K2 + kb * 256 + c * 16;
+      if (tail && kb * 128 + 8 * c >= a.K) off = 0x7FFFFFF0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (oc_lds_ptr)(smem + buf * kGemmXBuf + (16 * wave + j) * 1024), 16,
+                                               off, 0, 0, 0);
     }
   };
-  auto store_x = [&](uint16_t* xs) {
+  // Packed words and scale/zero words of one k-block: loaded two k-blocks
+  // ahead into one of three rotating register sets.  Each set costs exactly
+  // GemmLoads<BITS, CS>::n vector-memory instructions (no two of its loads are
+  // adjacent in memory, so none are merged), which the vmcnt waits rely on.
+  uint32_t w0[2][2][NWB], w1[2][2][NWB], w2[2][2][NWB];
+  uint32_t m0w[2][SPK], m1w[2][SPK], m2w[2][SPK];
+  auto load_w = [&](int kb, uint32_t (&wb)[2][2][NWB], uint32_t (&mw)[2][SPK]) {
+    using GG = Geo<BITS>;
+    const int u = kb / GG::U, kbl = kb % GG::U;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 512 * i, row = c >> 4, ch = c & 15;
-      *(oc_u4*)(xs + row * kGemmXS + ch * 8) = xr[i];
-    }
-  };
-  uint32_t wcur[4][NWB], wnxt[4][NWB];
-  uint32_t mcur[4][SPK], mnxt[4][SPK];
-  auto load_w = [&](int kb, uint32_t (&wbuf)[4][NWB], uint32_t (&mbuf)[4][SPK]) {
+    for (int T = 0; T < 2; ++T) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      load_kb_words<BITS>(a.w, a.NU, nt[j], kb, lane, wbuf[j]);
+      for (int q2 = 0; q2 < 2; ++q2) {
+        const uint8_t* base = a.w + ((size_t)(nt[T] * a.NU + u) * GG::P) * 1024 + cl[q2] * 16;
+        uint32_t* o = wb[T][q2];
+        if constexpr (BITS == 4 || BITS == 8) {
+#pragma unroll
+          for (int pt = 0; pt < GG::P; ++pt) {
+            const oc_u4 v = *(const oc_u4*)(base + pt * 1024);
+            o[4 * pt] = v[0];
+            o[4 * pt + 1] = v[1];
+            o[4 * pt + 2] = v[2];
+            o[4 * pt + 3] = v[3];
+          }
+        } else if constexpr (BITS == 2) {
+          typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+          const u2v v = *(const u2v*)(base + 8 * kbl);
+          o[0] = v[0];
+          o[1] = v[1];
+        } else {  // 3 words of k-block kbl inside the 12-word payload (3 parts of 4 words)
+#pragma unroll
+          for (int q = 0; q < 3; ++q) {
+            const int wi = 3 * kbl + q;
+            o[q] = *((const uint32_t*)(base + (wi >> 2) * 1024) + (wi & 3));
+          }
+        }
+      }
 #pragma unroll
       for (int q = 0; q < SPK; ++q) {
         const int k = kb * 128 + 32 * CS * q;
         const int g = min(a.gshift >= 0 ? (k >> a.gshift) : k / a.gs, a.G - 1);
-        mbuf[j][q] = a.meta[(size_t)g * a.N_pad + nt[j] * 16 + col];
+        mw[T][q] = a.meta[(size_t)g * a.N_pad + nt[T] * 16 + r16];
       }
     }
   };
+  // A-fragment byte offset of step s inside an x buffer (m-tile i adds 8 KB)
+  int xa[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) xa[s] = (lane & 31) * 256 + (((2 * s + h) ^ r16) * 16);
 
-  oc_f4 acc[8][4];
+  oc_f16v acc[8][2];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = oc_f4{0.f, 0.f, 0.f, 0.f};
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][T][r] = 0.f;
 
-  load_x(0);
-  load_w(0, wcur, mcur);
-  store_x(xs0);
+  // B operands of step s (both n32-tiles); dq holds the scale terms of the
+  // current group and is refreshed when a new group starts.
+  auto make_b = [&](const uint32_t (&wb)[2][2][NWB], const uint32_t (&mw)[2][SPK], int s, oc_u4 (&B)[2],
+                    GemmDeq<BF16> (&dq)[2]) {
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      if (s == 0 || (CS == 1 && (s & 1) == 0)) dq[T] = gemm_deq<BF16>(mw[T][(s >> 1) / CS]);
+      B[T] = gemm_apply<BF16>(decode_step<BITS, false>(wb[T][s & 1], s >> 1, msk, mag), dq[T]);
+    }
+  };
+  auto mma = [&](const oc_u4 (&A)[8], const oc_u4 (&B)[2]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int T = 0; T < 2; ++T) acc[i][T] = oc_mfma32<BF16>(A[i], B[T], acc[i][T]);
+  };
+  // One k-block: 8 steps of 16 k.  The A fragments and B operands of step
+  // s + 1 are read / dequantised while the 16 MFMAs of step s run; B of step 0
+  // (B0 on entry) was prepared before the barrier that opened this k-block.
+  auto compute = [&](int buf, const uint32_t (&wb)[2][2][NWB], const uint32_t (&mw)[2][SPK], oc_u4 (&B0)[2],
+                     GemmDeq<BF16> (&dq)[2]) {
+    const uint8_t* xb = smem + buf * kGemmXBuf;
+    auto read_a = [&](int s, oc_u4 (&A)[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) A[i] = *(const oc_u4*)(xb + xa[s] + i * 8192);
+    };
+    oc_u4 A0[8], A1[8], B1[2];
+    read_a(0, A0);
+#pragma unroll
+    for (int s = 0; s < 8; s += 2) {
+      read_a(s + 1, A1);
+      make_b(wb, mw, s + 1, B1, dq);
+      mma(A0, B0);
+      gemm_interleave();
+      if (s + 2 < 8) {
+        read_a(s + 2, A0);
+        make_b(wb, mw, s + 2, B0, dq);
+      }
+      mma(A1, B1);
+      gemm_interleave();
+    }
+  };
+
+  oc_u4 B0[2];
+  GemmDeq<BF16> dq[2];
+  constexpr int NW = GemmLoads<BITS, CS>::n;
+  // One k-block with register roles: wc/mc hold k-block kb, wn/mn k-block
+  // kb + 1 (in flight), wf/mf receive k-block kb + 2.  x of kb + 1 goes out
+  // first, so vmcnt(NW) at the end waits for it and for wn but not for wf.
+  // Loads past the last k-block re-read the last one (clamped index) so that
+  // every body issues the same instructions: the compiler's own waits stay
+  // exact and never fall back to waiting for everything.
+  const int last = a.NKB - 1;
+  auto body = [&](int kb, const uint32_t (&wc)[2][2][NWB], const uint32_t (&mc)[2][SPK],
+                  const uint32_t (&wn)[2][2][NWB], const uint32_t (&mn)[2][SPK], uint32_t (&wf)[2][2][NWB],
+                  uint32_t (&mf)[2][SPK]) {
+    const int buf = kb & 1;
+    load_x(min(kb + 1, last), buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(min(kb + 2, last), wf, mf);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf, wc, mc, B0, dq);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NW) : "memory");
+    make_b(wn, mn, 0, B0, dq);
+    // Plain s_barrier: __syncthreads() adds a workgroup release fence, which
+    // waits for every outstanding load (vmcnt(0)) including k-block kb + 2.
+    // LDS needs no fence: each wave's own x writes are complete (vmcnt above)
+    // and its LDS reads of the buffer refilled next were consumed by MFMAs.
+    asm volatile("s_barrier" ::: "memory");
+  };
+
+  load_x(0, 0);
+  load_w(0, w0, m0w);
+  load_w(min(1, last), w1, m1w);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  make_b(w0, m0w, 0, B0, dq);
   __syncthreads();
-  const uint16_t* xcur = xs0;
-  uint16_t* xnext = xs1;
-  for (int kb = 0; kb < a.NKB; ++kb) {
-    const bool more = kb + 1 < a.NKB;
-    if (more) {
-      load_x(kb + 1);
-      load_w(kb + 1, wnxt, mnxt);
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      // one MFMA step: the 4 n-tiles' B operands, then 8 m-tiles
-      oc_u4 bw[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t md = mcur[j][t / CS];
-        const uint16_t sh = (uint16_t)(md & 0xFFFFu);
-        const float sf = oc_h2f(sh);
-        const float zoff = OFF + (float)(md >> 16);
-        if constexpr (BF16 && BITS == 4) {
-          bw[j] = dequant_step_b4_bf16(wcur[j][t], sf, -sf * (float)(md >> 16));
-        } else if constexpr (BF16 && BITS == 8) {
-          bw[j] = dequant_step_b8_bf16(wcur[j][2 * t], wcur[j][2 * t + 1], sf, -sf * (float)(md >> 16));
-        } else {
-          const oc_u4 bq = decode_step<BITS, BF16>(wcur[j], t, msk, mag);
-          uint32_t s_h2 = 0, ozz_h2 = 0;
-          float cf = 0.f;
-          if constexpr (BF16) {
-            cf = -sf * zoff;  // exact: 11-bit scale times a <= 9-bit integer
-          } else {
-            s_h2 = (uint32_t)sh | ((uint32_t)sh << 16);
-            const uint16_t oz = oc_f2h(zoff);
-            ozz_h2 = (uint32_t)oz | ((uint32_t)oz << 16);
-          }
-#pragma unroll
-          for (int p = 0; p < 4; ++p) bw[j][p] = dequant_pair<BF16>(bq[p], ozz_h2, s_h2, sf, cf);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const oc_u4 av = *(const oc_u4*)(xcur + (i * 16 + col) * kGemmXS + 32 * t + 8 * kq);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = oc_mfma16<BF16>(av, bw[j], acc[i][j]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (more) store_x(xnext);
-    __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int q = 0; q < NWB; ++q) wcur[j][q] = wnxt[j][q];
-#pragma unroll
-        for (int q = 0; q < SPK; ++q) mcur[j][q] = mnxt[j][q];
-      }
-      const uint16_t* tmp = xcur;
-      xcur = xnext;
-      xnext = (uint16_t*)tmp;
-    }
+  const int groups = a.NKB / 3;
+  for (int g = 0; g < groups; ++g) {
+    body(3 * g, w0, m0w, w1, m1w, w2, m2w);
+    body(3 * g + 1, w1, m1w, w2, m2w, w0, m0w);
+    body(3 * g + 2, w2, m2w, w0, m0w, w1, m1w);
   }
+  if (a.NKB % 3 >= 1) body(3 * groups, w0, m0w, w1, m1w, w2, m2w);
+  if (a.NKB % 3 == 2) body(3 * groups + 1, w1, m1w, w2, m2w, w0, m0w);
+  // the last body prefetched into the idle x buffer: let it land before exit
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // epilogue: lane holds rows 16i + 4kq + r of column 16 nt + col
+  // epilogue: register r of tile (i, T) is row 32i + 8(r/4) + 4h + r%4, column n0 + 32T + lane%32
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = (nt0 + j) * 16 + col;
+  for (int T = 0; T < 2; ++T) {
+    const int n = n0 + 32 * T + (lane & 31);
     if (n >= a.N) continue;
     float b = 0.f;
     if (a.bias) b = BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + i * 16 + 4 * kq + r;
-        if (m < a.M) a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(acc[i][j][r] + b) : oc_f2h(acc[i][j][r] + b);
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M) a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(acc[i][T][r] + b) : oc_f2h(acc[i][T][r] + b);
       }
   }
 }
@@ -816,21 +897,21 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     g.gs = gs;
     g.gshift = log2_exact(gs);
     g.NKB = L.K_pad / 128;
+    const bool cs4 = (gs % 128) == 0;
     g.MB = (M + kGemmBM - 1) / kGemmBM;
     g.NB = (L.N_pad + kGemmBN - 1) / kGemmBN;
-    const size_t lds = (size_t)2 * kGemmBM * kGemmXS * 2;
     const dim3 grid(g.MB * g.NB);
-    const bool cs4 = (gs % 128) == 0;
+    const size_t lds = 2 * kGemmXBuf;
     switch (bits) {
-#define OC_GM(B_)                                                                                  \
-  case B_:                                                                                         \
-    if (bf16) {                                                                                    \
-      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, true>), grid, dim3(512), lds, st, g);             \
-      else hipLaunchKernelGGL((k_gemm<B_, 1, true>), grid, dim3(512), lds, st, g);                 \
-    } else {                                                                                       \
-      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, false>), grid, dim3(512), lds, st, g);            \
-      else hipLaunchKernelGGL((k_gemm<B_, 1, false>), grid, dim3(512), lds, st, g);                \
-    }                                                                                              \
+#define OC_GM(B_)                                                                                 \
+  case B_:                                                                                        \
+    if (bf16) {                                                                                   \
+      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, true>), grid, dim3(256), lds, st, g);            \
+      else hipLaunchKernelGGL((k_gemm<B_, 1, true>), grid, dim3(256), lds, st, g);                \
+    } else {                                                                                      \
+      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, false>), grid, dim3(256), lds, st, g);           \
+      else hipLaunchKernelGGL((k_gemm<B_, 1, false>), grid, dim3(256), lds, st, g);               \
+    }                                                                                             \
     break;
       OC_GM(2) OC_GM(3) OC_GM(4) OC_GM(8)
 #undef OC_GM

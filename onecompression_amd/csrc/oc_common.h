@@ -113,6 +113,19 @@ __device__ __forceinline__ oc_f4 oc_mfma16(oc_u4 a, oc_u4 b, oc_f4 c) {
   }
 }
 
+// 32x32x16 MFMA: lane l holds A row l%32 / B column l%32, k = 8(l/32) .. +7;
+// D register r of lane l is row 8(r/4) + 4(l/32) + r%4, column l%32.
+template <bool BF16>
+__device__ __forceinline__ oc_f16v oc_mfma32(oc_u4 a, oc_u4 b, oc_f16v c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(oc_bf168, a),
+                                                   __builtin_bit_cast(oc_bf168, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(oc_half8, a),
+                                                  __builtin_bit_cast(oc_half8, b), c, 0, 0, 0);
+  }
+}
+
 __device__ __forceinline__ float oc_h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
