@@ -737,12 +737,15 @@ GemvPlan plan_gemv(const oc::Layout& L, int M, int gs) {
   // x chunks of 16 B per lane per unit: M rows x 16U chunks over 64 lanes
   const int xc = (M * 16 * L.U + 63) / 64;
   p.xch = xc <= 1 ? 1 : (xc <= 4 ? 4 : (xc <= 8 ? 8 : 16));
-  p.nt = (env_int("OC_GEMV_NT", 1) == 2 && p.xch == 1) ? 2 : 1;
+  // Two n-tiles per workgroup when there are enough column groups left to
+  // fill the GPU: fewer, longer waves (measured better on 3-bit gate/up).
+  const int nt_env = env_int("OC_GEMV_NT", 0);
+  p.nt = (p.xch == 1 && (nt_env == 2 || (nt_env == 0 && (L.NT + 1) / 2 >= 384))) ? 2 : 1;
   p.ngroups = (L.NT + p.nt - 1) / p.nt;
   // One workgroup streams the whole K of its columns; few column groups get
   // more waves per workgroup.  Each wave owns an x slot of M x (128U + 8) halfs.
   int w = env_int("OC_GEMV_W", 0);
-  if (w != 4 && w != 8 && w != 16) w = p.ngroups >= 512 ? 8 : 16;
+  if (w != 4 && w != 8 && w != 16) w = (p.ngroups >= 512 || p.nt == 2) ? 8 : 16;
   if (p.cs == 1 && w == 16) w = 8;
   if (p.xch > 1 && w == 16) w = 8;
   const size_t slot = (size_t)M * (L.U * 128 + 8) * 2;

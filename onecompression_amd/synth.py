@@ -88,6 +88,43 @@ CONFIG4 = [  # Qwen3-14B prefill, 4-bit, bf16 activations
 ]
 
 
+def fuse_cases(cases, name: str) -> GPTQCase:
+    """Concatenate same-K, same-bits, no-act-order projections along N.
+
+    This is how vLLM stores a merged layer (QKVParallelLinear /
+    MergedColumnParallelLinear): one qweight/qzeros/scales whose output
+    columns are the shards side by side, served by one apply() call.
+    """
+    c0 = cases[0]
+    for c in cases:
+        if (c.in_features, c.bits, c.group_size, c.act_order) != (c0.in_features, c0.bits, c0.group_size, False):
+            raise ValueError(f"cannot fuse {c.name} with {c0.name}")
+        if (c.out_features * c.bits) % 32:
+            raise ValueError(f"{c.name}: N * bits must be a multiple of 32 to concatenate packed zeros")
+    return GPTQCase(name, c0.in_features, sum(c.out_features for c in cases), c0.bits, c0.group_size, False,
+                    torch.cat([c.qweight for c in cases], dim=1), torch.cat([c.qzeros for c in cases], dim=1),
+                    torch.cat([c.scales for c in cases], dim=1), None)
+
+
+# Projections that read the same input and share bits / group size run as one
+# merged layer, as vLLM builds them (q stays alone when its bits differ).
+LAYER_GROUPS = {1: [("q_proj",), ("k_proj", "v_proj"), ("o_proj",), ("gate_proj", "up_proj"), ("down_proj",)]}
+
+
+def layer_cases(cfg: int, seed: int = 0):
+    """The apply() calls of one decoder layer: config cases, merged per LAYER_GROUPS."""
+    cases = config_cases(cfg, seed)
+    groups = LAYER_GROUPS.get(cfg)
+    if groups is None:
+        return cases
+    by_name = {c.name: c for c in cases}
+    out = []
+    for g in groups:
+        out.append(by_name[g[0]] if len(g) == 1 else fuse_cases([by_name[n] for n in g], "_".join(
+            [g[0].replace("_proj", "")] + [n.replace("_proj", "") for n in g[1:]]) + "_proj"))
+    return out
+
+
 def config_cases(cfg: int, seed: int = 0):
     spec = {0: CONFIG0, 1: CONFIG1, 2: CONFIG2, 4: CONFIG4}[cfg]
     act = cfg == 2
