@@ -141,8 +141,17 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     tflops = 2.0 * m * k * n / (ms * 1e-3) / 1e12
-    return {"workload": f"cfg4 {name} {k}->{n} {bits}b gs128 bf16", "M": m, "ms": ms,
-            "TFLOPs": tflops, "frac_mfma_peak": tflops / MFMA_F16_PEAK_TFLOPS}
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("kernels", {}).get(f"k_gemm {name} {k}->{n} {bits}b M={m}")
+    return {"workload": f"cfg4 {name} {k}->{n} {bits}b gs128 bf16", "M": m, "ms": round(ms, 4),
+            "TFLOPs": round(tflops, 1), "frac_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                         "traffic": traffic, "kernel": f"k_gemm<{bits},4,true>",
+                         "avg_us": round(ms * 1e3, 1)}}
 
 
 def cpu_baseline(cases, m, budget_s=20.0):
@@ -185,6 +194,8 @@ def main():
     ap.add_argument("--m", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the M=2048 dequant-GEMM measurement (config 4 gate_up, bf16)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -204,6 +215,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
+        return
+    if args.gemm_only:
+        print(json.dumps(bench_gemm_large(2048, args.steps, args.warmup, dev)))
         return
     r = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev)
     dom = max(r["kernels"], key=lambda k: k["us"])

@@ -717,7 +717,7 @@ int dispatch_skinny_bits(int bits, const SkinnyPlan& p, const SkinnyArgs& a, hip
 }
 
 struct GemvPlan {
-  int nt, w, cs, S, ups, ngroups, xch;
+  int nt, w, cs, S, ups, ngroups, xch, deep;
   size_t lds;
 };
 
@@ -751,6 +751,7 @@ GemvPlan plan_gemv(const oc::Layout& L, int M, int gs) {
   const size_t slot = (size_t)M * (L.U * 128 + 8) * 2;
   while (w > 4 && slot * w > kGemvLds) w /= 2;
   p.w = w;
+  p.deep = env_int("OC_GEMV_DEEP", 0);
   int S = env_int("OC_GEMV_S", 1);
   S = S < 1 ? 1 : (S > L.NU ? L.NU : S);
   p.ups = (L.NU + S - 1) / S;
@@ -773,6 +774,15 @@ int launch_gemv(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
     OC_HIP(hipGetLastError());                                                                      \
     return 0;                                                                                       \
   }
+#define OC_GVD(NT_, W_)                                                                               \
+  if (p.deep && p.nt == NT_ && p.cs == 4 && p.w == W_ && p.xch == 1) {                               \
+    constexpr int D_ = 2 * (DB / NT_ > 0 ? DB / NT_ : 1);                                            \
+    hipLaunchKernelGGL((k_gemv<BITS, NT_, 4, D_, W_, 1, BF16>), grid, dim3(64 * W_), p.lds, st, a);  \
+    OC_HIP(hipGetLastError());                                                                       \
+    return 0;                                                                                        \
+  }
+  OC_GVD(2, 8) OC_GVD(2, 4) OC_GVD(1, 4)
+#undef OC_GVD
   OC_GV(1, 4, 16, 1) OC_GV(2, 4, 16, 1)
   OC_GV(1, 4, 8, 1) OC_GV(1, 1, 8, 1) OC_GV(2, 4, 8, 1) OC_GV(2, 1, 8, 1)
   OC_GV(1, 4, 4, 1) OC_GV(1, 1, 4, 1) OC_GV(2, 4, 4, 1) OC_GV(2, 1, 4, 1)
