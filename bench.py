@@ -154,35 +154,170 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
                          "avg_us": round(ms * 1e3, 1)}}
 
 
-def cpu_baseline(cases, m, budget_s=20.0):
-    """OneComp's CPU path (checkpoint.py:186-259 + torch.matmul) on the host cores."""
+RIDGE_FLOP_PER_BYTE = MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+
+
+def _time_graph(launch, copies, iters, warm=2):
+    """Mean µs per launch of `iters` launches (launch(i) uses copy i % copies) in one HIP graph."""
+    import torch
+
+    for i in range(warm):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / iters
+
+
+def _entry(cfg, name, k, n, m, bits, nbytes, flops, us, dtype):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    tfs = flops / (us * 1e-6) / 1e12
+    bound = "hbm" if flops / nbytes < RIDGE_FLOP_PER_BYTE else "mfma"
+    return {"cfg": cfg, "layer": name, "K": k, "N": n, "bits": bits, "M": m, "dtype": dtype,
+            "us": round(us, 2), "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "TFLOPs": round(tfs, 2), "frac_mfma_peak": round(tfs / MFMA_F16_PEAK_TFLOPS, 4), "bound": bound}
+
+
+def _rotation(weight_bytes, ms, rotate_bytes=1 << 30):
+    """Weight copies for a layer: enough to exceed the MALL when any M is HBM-bound."""
+    return max(1, min(32, -(-rotate_bytes // weight_bytes))) if min(ms) <= 64 else 1
+
+
+def report_configs(dev):
+    """BASELINE configs 0-4 at every listed M: µs per apply(), GB/s, TFLOP/s, binding roof."""
+    import torch
+
+    from onecompression_amd import dbf_ops, ops, synth
+
+    out = []
+    plan = [(0, synth.config_cases(0), (1, 16), torch.float16),
+            (1, synth.layer_cases(1), (1, 8, 32, 128), torch.float16),
+            (2, synth.config_cases(2), (1, 16, 64, 256), torch.float16),
+            (4, synth.config_cases(4), (2048, 4096, 8192), torch.bfloat16)]
+    for cfg, cases, ms, dt in plan:
+        dname = "fp16" if dt == torch.float16 else "bf16"
+        for c in cases:
+            cd = c.to(dev)
+            p0 = ops.gptq_prepare(cd.qweight, cd.qzeros, cd.scales, cd.g_idx, c.bits, c.group_size)
+            del cd
+            preps = [p0] + [ops.PreparedGPTQ(p0.packed.clone(), p0.meta.clone(), p0.perm, p0.in_features,
+                                             p0.out_features, p0.bits, p0.group_size, p0.num_groups)
+                            for _ in range(_rotation(c.weight_bytes(), ms) - 1)]
+            for m in ms:
+                x = synth.activations(m, c.in_features, dt, seed=200 + m).to(dev)
+                y = torch.empty((m, c.out_features), dtype=dt, device=dev)
+                iters = 64 if m <= 256 else 8
+                us = _time_graph(lambda i: ops.gptq_gemm(x, preps[i % len(preps)], out=y), len(preps), iters)
+                out.append(_entry(cfg, c.name, c.in_features, c.out_features, m, c.bits,
+                                  _gptq_bytes(c, m), 2.0 * m * c.in_features * c.out_features, us, dname))
+            del preps, p0
+            torch.cuda.empty_cache()
+    # config 3: one DBF path and the two-path MDBF variant, per shape
+    for i, (name, k, n) in enumerate(synth.CONFIG3):
+        cases = [synth.dbf_case(name, k, n, 1.0, seed=300 + 2 * i + j) for j in range(2)]
+        ms = (1, 32, 512)
+        copies = _rotation(sum(c.weight_bytes() for c in cases), ms)
+        parts, paths = [], []
+        for rep in range(copies):
+            row_p, row_m = [], []
+            for c in cases:
+                cd = c.to(dev)
+                row_p.append(dbf_ops.dbf_prepare(cd.s0, cd.bp1, cd.s2, cd.bp3, cd.s4, k, c.mid, n))
+                row_m.append(dbf_ops.mdbf_prepare_path(
+                    cd.bp3, (n, c.mid), cd.bp1, (c.mid, k), cd.s4.view(n, 1), cd.s0.view(k, 1),
+                    cd.s2.view(c.mid, 1), torch.ones((c.mid, 1), dtype=torch.float16, device=dev)))
+            parts.append(row_p[0])
+            paths.append(row_m)
+        for m in ms:
+            x = synth.activations(m, k, torch.float16, seed=400 + m).to(dev)
+            iters = 64 if m <= 32 else 16
+            c = cases[0]
+            byt = c.weight_bytes() + 2 * m * (k + n)
+            fl = 2.0 * m * c.mid * (k + n)
+            us = _time_graph(lambda j: dbf_ops.dbf_forward(x, [parts[j % copies]]), copies, iters)
+            out.append(_entry(3, f"dbf {name}", k, n, m, 1, byt, fl, us, "fp16"))
+            byt2 = sum(cc.weight_bytes() for cc in cases) + 2 * m * (k + n)
+            us = _time_graph(lambda j: dbf_ops.mdbf_forward(x, paths[j % copies]), copies, iters)
+            out.append(_entry(3, f"mdbf P=2 {name}", k, n, m, 1, byt2, 2 * fl, us, "fp16"))
+        del parts, paths
+        torch.cuda.empty_cache()
+    return out
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cases, m, budget_s=20.0, min_runs=3, max_runs=10, warmup=1):
+    """OneComp's CPU path (checkpoint.py:186-259 + torch.matmul) on the host cores.
+
+    Per run: for every layer, the oracle's unpack + v1 zero restore + fp32
+    dequant (timed as `dequant`), then torch.matmul(x, W.T) in fp32 (`matmul`).
+    Runs stop at max_runs or once budget_s is spent (never below min_runs).
+    """
     import numpy as np
     import torch
 
     from oracle import gptq as og
 
+    torch.set_num_threads(os.cpu_count() or 1)
     threads = torch.get_num_threads()
-    x = [np.random.default_rng(i).normal(size=(m, c.in_features)).astype(np.float32) for i, c in enumerate(cases)]
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
+    x = [torch.from_numpy(np.random.default_rng(i).normal(size=(m, c.in_features)).astype(np.float32))
+         for i, c in enumerate(cases)]
+
+    def run():
+        td = tm = 0.0
         for c, xi in zip(cases, x):
+            t0 = time.perf_counter()
             qw, qz, sc = c.qweight.numpy(), c.qzeros.numpy(), c.scales.numpy()
             q = og.unpack_int_weights(qw, c.bits, (c.out_features, c.in_features))
             z = og.restore_zeros(og.unpack_zeros(qz, c.bits, c.out_features), c.bits, "gptq")
             g = og.default_g_idx(c.in_features, c.group_size) if c.g_idx is None else c.g_idx.numpy()
-            w = og.dequant_fp32(q, sc, z, g)
-            torch.matmul(torch.from_numpy(xi), torch.from_numpy(w).T)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 3:
-            break
-    t = statistics.median(times)
+            w = torch.from_numpy(og.dequant_fp32(q, sc, z, g))
+            t1 = time.perf_counter()
+            torch.matmul(xi, w.T)
+            td += t1 - t0
+            tm += time.perf_counter() - t1
+        return td, tm
+
+    for _ in range(warmup):
+        run()
+    runs = []
+    t_start = time.perf_counter()
+    while len(runs) < max_runs and (len(runs) < min_runs or time.perf_counter() - t_start < budget_s):
+        runs.append(run())
+    tot = statistics.median(d + mm for d, mm in runs)
     step_bytes = sum(_gptq_bytes(c, m) for c in cases)
-    return {"value": step_bytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} full step(s) of the same workload (all 7 projections, M={m}); "
-                      f"median {t:.2f} s/step; numpy unpack+dequant then torch.matmul fp32, "
-                      f"torch threads={threads}, os.cpu_count={os.cpu_count()}"}
+    return {"value": step_bytes / tot / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "median_s": round(tot, 4), "dequant_s": round(statistics.median(d for d, _ in runs), 4),
+            "matmul_s": round(statistics.median(mm for _, mm in runs), 4), "runs": len(runs),
+            "warmup": warmup,
+            "sample": f"{len(runs)} full step(s) after {warmup} warmup of the same workload "
+                      f"({len(cases)} layers, M={m}); numpy unpack + v1 restore + fp32 dequant, then "
+                      f"torch.matmul fp32 on {threads} threads"}
+
+
+def synth_config0():
+    from onecompression_amd import synth
+
+    return synth.config_cases(0)
 
 
 def main():
@@ -194,6 +329,8 @@ def main():
     ap.add_argument("--m", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config report (BASELINE configs 0-4 at every M)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the M=2048 dequant-GEMM measurement (config 4 gate_up, bf16)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -258,8 +395,16 @@ def main():
             out["secondary"] = bench_gemm_large(2048, 5, 2, dev)
         except Exception as e:  # the large-M measurement is reported, never hides the main line
             out["secondary"] = {"error": str(e)}
+    if not args.no_configs:
+        try:
+            out["configs"] = report_configs(dev)
+        except Exception as e:  # reported, never hides the main line
+            out["configs"] = {"error": str(e)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(r["cases"], args.m)
+        c0 = synth_config0()
+        out["cpu_baseline_cfg0"] = {f"M={mm}": cpu_baseline(c0, mm, budget_s=15.0, min_runs=10, max_runs=10,
+                                                             warmup=2) for mm in (1, 16)}
     print(json.dumps(out))
 
 

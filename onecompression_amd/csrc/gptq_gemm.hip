@@ -330,8 +330,25 @@ struct GemmArgs {
   const uint32_t* meta;
   const uint16_t* bias;
   uint16_t* y;
+  float* part;  // fp32 partial tiles of the K-split pieces (tiles_main.. onwards)
   int M, K, N, N_pad, NT_total, NU, G, gs, gshift, NKB, MB, NB;
+  int tiles_main;  // workgroups below this index compute a whole tile
+  int S, kper;     // the remaining tiles are split into S pieces of kper k-blocks
 };
+
+// Tile order: consecutive workgroups go to consecutive XCDs; with 8 | MB the
+// 8 XCDs take 8 M-blocks of one column block at once (shared weights) and
+// the CUs of one XCD share an M-block (x stays in that XCD's L2).
+__device__ __forceinline__ void gemm_tile(int t, int MB, int NB, int& mb, int& nb) {
+  if ((MB % 8) == 0) {
+    const int xcd = t & 7, j = t >> 3;
+    mb = (j / NB) * 8 + xcd;
+    nb = j % NB;
+  } else {
+    mb = t / NB;
+    nb = t % NB;
+  }
+}
 
 // Packed words of one k-block per lane and chunk (lane-chunk layout of oc_common.h).
 template <int BITS>
@@ -448,15 +465,14 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, r16 = lane & 15;
   const int L = blockIdx.x;
+  // whole tile, or piece `split` of a tile cut along K
+  const bool piece = L >= a.tiles_main;
+  const int pidx = L - a.tiles_main;
+  const int tile = piece ? a.tiles_main + pidx / a.S : L;
+  const int kb0 = piece ? (pidx % a.S) * a.kper : 0;
+  const int kb1 = piece ? min(kb0 + a.kper, a.NKB) : a.NKB;
   int mb, nb;
-  if ((a.MB % 8) == 0) {
-    const int xcd = L & 7, j = L >> 3;
-    mb = (j / a.NB) * 8 + xcd;
-    nb = j % a.NB;
-  } else {
-    mb = L / a.NB;
-    nb = L % a.NB;
-  }
+  gemm_tile(tile, a.MB, a.NB, mb, nb);
   const int m0 = mb * kGemmBM;
   const int n0 = nb * kGemmBN + wave * 64;  // first column of this wave
   int nt[2], cl[2];
@@ -599,11 +615,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   // Loads past the last k-block re-read the last one (clamped index) so that
   // every body issues the same instructions: the compiler's own waits stay
   // exact and never fall back to waiting for everything.
-  const int last = a.NKB - 1;
+  const int last = kb1 - 1;
   auto body = [&](int kb, const uint32_t (&wc)[2][2][NWB], const uint32_t (&mc)[2][SPK],
                   const uint32_t (&wn)[2][2][NWB], const uint32_t (&mn)[2][SPK], uint32_t (&wf)[2][2][NWB],
                   uint32_t (&mf)[2][SPK]) {
-    const int buf = kb & 1;
+    const int buf = (kb - kb0) & 1;
     load_x(min(kb + 1, last), buf ^ 1);
     __builtin_amdgcn_sched_barrier(0);
     load_w(min(kb + 2, last), wf, mf);
@@ -618,23 +634,34 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     asm volatile("s_barrier" ::: "memory");
   };
 
-  load_x(0, 0);
-  load_w(0, w0, m0w);
-  load_w(min(1, last), w1, m1w);
+  load_x(kb0, 0);
+  load_w(kb0, w0, m0w);
+  load_w(min(kb0 + 1, last), w1, m1w);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   make_b(w0, m0w, 0, B0, dq);
   __syncthreads();
-  const int groups = a.NKB / 3;
+  const int nkb = kb1 - kb0, groups = nkb / 3;
   for (int g = 0; g < groups; ++g) {
-    body(3 * g, w0, m0w, w1, m1w, w2, m2w);
-    body(3 * g + 1, w1, m1w, w2, m2w, w0, m0w);
-    body(3 * g + 2, w2, m2w, w0, m0w, w1, m1w);
+    body(kb0 + 3 * g, w0, m0w, w1, m1w, w2, m2w);
+    body(kb0 + 3 * g + 1, w1, m1w, w2, m2w, w0, m0w);
+    body(kb0 + 3 * g + 2, w2, m2w, w0, m0w, w1, m1w);
   }
-  if (a.NKB % 3 >= 1) body(3 * groups, w0, m0w, w1, m1w, w2, m2w);
-  if (a.NKB % 3 == 2) body(3 * groups + 1, w1, m1w, w2, m2w, w0, m0w);
+  if (nkb % 3 >= 1) body(kb0 + 3 * groups, w0, m0w, w1, m1w, w2, m2w);
+  if (nkb % 3 == 2) body(kb0 + 3 * groups + 1, w1, m1w, w2, m2w, w0, m0w);
   // the last body prefetched into the idle x buffer: let it land before exit
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  if (piece) {
+    // fp32 partial tile in register order [wave][i][T][r][lane]: 256-B stores
+    float* pp = a.part + (size_t)pidx * (kGemmBM * kGemmBN) + wave * (8 * 2 * 16 * 64) + lane;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pp[((i * 2 + T) * 16 + r) * 64] = acc[i][T][r];
+    return;
+  }
   // epilogue: register r of tile (i, T) is row 32i + 8(r/4) + 4h + r%4, column n0 + 32T + lane%32
 #pragma unroll
   for (int T = 0; T < 2; ++T) {
@@ -650,6 +677,26 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
         if (m < a.M) a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(acc[i][T][r] + b) : oc_f2h(acc[i][T][r] + b);
       }
   }
+}
+
+// y for the K-split tiles: the S fp32 partial tiles summed in split order
+// (deterministic) plus bias.  One thread per element of a 256 x 256 tile, in
+// the partials' register order.
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_gemm_fixup(const GemmArgs a) {
+  const int t = blockIdx.y;  // split tile
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int lane = e & 63, r = (e >> 6) & 15, T = (e >> 10) & 1, i = (e >> 11) & 7, wave = e >> 14;
+  int mb, nb;
+  gemm_tile(a.tiles_main + t, a.MB, a.NB, mb, nb);
+  const int m = mb * kGemmBM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+  const int n = nb * kGemmBN + 64 * wave + 32 * T + (lane & 31);
+  if (m >= a.M || n >= a.N) return;
+  const float* pp = a.part + (size_t)t * a.S * (kGemmBM * kGemmBN) + e;
+  float v = 0.f;
+  for (int s = 0; s < a.S; ++s) v += pp[(size_t)s * (kGemmBM * kGemmBN)];
+  if (a.bias) v += BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
+  a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(v) : oc_f2h(v);
 }
 
 // x_perm[m, p] = x[m, perm[p]] (act-order activations, 16-bit elements).
@@ -820,6 +867,52 @@ int launch_reduce(bool bf16, const float* partial, int S, int M, int N, int N_pa
 
 constexpr int kSkinnyMaxM = 64;
 
+// Large-M tiling: whole 256 x 256 tiles, except that a last round of tiles
+// that would leave more than half of the CUs idle is cut along K into S
+// pieces (at least 4 k-blocks each) whose fp32 partials k_gemm_fixup sums.
+struct GemmPlan {
+  int MB, NB, NKB, tiles_main, split_tiles, S, kper;
+  size_t part_bytes;
+};
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cus[dev] = c;
+  }
+  return cus[dev];
+}
+
+GemmPlan plan_gemm(const oc::Layout& L, int M) {
+  GemmPlan p;
+  p.MB = (M + kGemmBM - 1) / kGemmBM;
+  p.NB = (L.N_pad + kGemmBN - 1) / kGemmBN;
+  p.NKB = L.K_pad / 128;
+  const int T = p.MB * p.NB, C = device_cus();
+  const int rem = T % C;
+  p.tiles_main = T;
+  p.split_tiles = 0;
+  p.S = 1;
+  p.kper = p.NKB;
+  int S = rem > 0 && 2 * rem <= C ? C / rem : 1;
+  const int env = env_int("OC_GEMM_SPLIT", 0);
+  if (env > 0) S = env;
+  if (S > 8) S = 8;
+  while (S > 1 && p.NKB / S < 4) --S;
+  if (rem > 0 && S > 1) {
+    p.kper = (p.NKB + S - 1) / S;
+    p.S = (p.NKB + p.kper - 1) / p.kper;
+    p.split_tiles = rem;
+    p.tiles_main = T - rem;
+  }
+  p.part_bytes = (size_t)p.split_tiles * p.S * kGemmBM * kGemmBN * 4;
+  return p;
+}
+
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 }  // namespace
@@ -835,7 +928,7 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
     if (p.S > 1) ws += align256((size_t)p.S * M * L.N_pad * 4);
     return ws;
   }
-  if (M >= env_int("OC_GEMM_MIN_M", 128)) return ws;
+  if (M >= env_int("OC_GEMM_MIN_M", 128)) return ws + align256(plan_gemm(L, M).part_bytes);
   const int Mc = M < kSkinnyMaxM ? M : kSkinnyMaxM;
   const SkinnyPlan p = plan_skinny(L, Mc);
   if (p.S > 1) ws += align256((size_t)p.S * Mc * L.N_pad * 4);
@@ -911,9 +1004,14 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     g.gshift = log2_exact(gs);
     g.NKB = L.K_pad / 128;
     const bool cs4 = (gs % 128) == 0;
-    g.MB = (M + kGemmBM - 1) / kGemmBM;
-    g.NB = (L.N_pad + kGemmBN - 1) / kGemmBN;
-    const dim3 grid(g.MB * g.NB);
+    const GemmPlan gp = plan_gemm(L, M);
+    g.MB = gp.MB;
+    g.NB = gp.NB;
+    g.tiles_main = gp.tiles_main;
+    g.S = gp.S;
+    g.kper = gp.kper;
+    g.part = (float*)ws;
+    const dim3 grid(gp.tiles_main + gp.split_tiles * gp.S);
     const size_t lds = 2 * kGemmXBuf;
     switch (bits) {
 #define OC_GM(B_)                                                                                 \
@@ -930,6 +1028,12 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
 #undef OC_GM
     }
     OC_HIP(hipGetLastError());
+    if (gp.split_tiles > 0) {
+      const dim3 fgrid(kGemmBM * kGemmBN / 256, gp.split_tiles);
+      if (bf16) hipLaunchKernelGGL(k_gemm_fixup<true>, fgrid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL(k_gemm_fixup<false>, fgrid, dim3(256), 0, st, g);
+      OC_HIP(hipGetLastError());
+    }
     return 0;
   }
   // Rows are processed in chunks of at most 64 by the skinny kernel.

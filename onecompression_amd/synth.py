@@ -129,3 +129,52 @@ def config_cases(cfg: int, seed: int = 0):
     spec = {0: CONFIG0, 1: CONFIG1, 2: CONFIG2, 4: CONFIG4}[cfg]
     act = cfg == 2
     return [gptq_case(name, k, n, b, 128, act, seed + i) for i, (name, k, n, b) in enumerate(spec)]
+
+
+# DBF / MDBF (config 3) ---------------------------------------------------------------------
+CONFIG3 = [("up_proj", 4096, 14336), ("down_proj", 14336, 4096)]
+
+
+def dbf_rank(bits: float, k: int, n: int) -> int:
+    """DBF rank as the reference computes it (int() truncation, capped at min(K, N))."""
+    return min(min(k, n), int(bits * k * n / (k + n)))
+
+
+def _signs(gen, rows: int, cols: int) -> torch.Tensor:
+    """rows x cols +-1 factor bit-packed MSB-first, flat (uniform random bits)."""
+    nbytes = (rows * cols + 7) // 8
+    return torch.randint(0, 256, (nbytes,), generator=gen, dtype=torch.int64).to(torch.uint8)
+
+
+def _vec(gen, n: int) -> torch.Tensor:
+    return (torch.randn(n, generator=gen).abs() * 0.05 + 1e-3).to(torch.float16)
+
+
+@dataclass
+class DBFCase:
+    """One DBF path W = diag(s4) S1 diag(s2) S2 diag(s0) in the checkpoint layout."""
+
+    name: str
+    in_features: int
+    out_features: int
+    mid: int
+    s0: torch.Tensor   # fp16 [K]
+    bp1: torch.Tensor  # uint8, S2 (r x K)
+    s2: torch.Tensor   # fp16 [r]
+    bp3: torch.Tensor  # uint8, S1 (N x r)
+    s4: torch.Tensor   # fp16 [N]
+
+    def weight_bytes(self) -> int:
+        return (self.bp1.numel() + self.bp3.numel() +
+                2 * (self.in_features + self.mid + self.out_features))
+
+    def to(self, dev):
+        return DBFCase(self.name, self.in_features, self.out_features, self.mid, self.s0.to(dev),
+                       self.bp1.to(dev), self.s2.to(dev), self.bp3.to(dev), self.s4.to(dev))
+
+
+def dbf_case(name: str, k: int, n: int, bits: float = 1.0, seed: int = 0) -> DBFCase:
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    r = dbf_rank(bits, k, n)
+    return DBFCase(name, k, n, r, _vec(gen, k), _signs(gen, r, k), _vec(gen, r), _signs(gen, n, r),
+                   _vec(gen, n))

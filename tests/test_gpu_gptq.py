@@ -182,3 +182,36 @@ def test_gemm_large_m(dev, bits, m, k, n, gs, act, dtype):
 def test_gemm_large_m_config4_shape(dev):
     c = synth.gptq_case("o", 5120, 5120, 4, 128, False, seed=3)
     _gemm_check(dev, c, 512, "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_gemm_split_tail(dev, monkeypatch, dtype):
+    """260 tiles of 256 x 256 on a 256-CU part: 256 whole tiles plus 4 tiles cut
+    along K whose fp32 partials k_gemm_fixup sums (with bias).  The split result
+    matches the unsplit launch and, on the tail tiles' columns, the oracle."""
+    k, n, m = 1024, 66560, 130
+    c = synth.gptq_case("t", k, n, 4, 128, False, seed=91)
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    cd = c.to(dev)
+    prep = ops.gptq_prepare(cd.qweight, cd.qzeros, cd.scales, None, 4, 128)
+    x = synth.activations(m, k, td, seed=5).to(dev)
+    b = (torch.randn(n) * 0.1).to(td).to(dev)
+    y = ops.gptq_gemm(x, prep, b)
+    assert torch.equal(ops.gptq_gemm(x, prep, b), y)  # deterministic split order
+    monkeypatch.setenv("OC_GEMM_SPLIT", "1")
+    prep._ws.clear()
+    y1 = ops.gptq_gemm(x, prep, b)
+    torch.cuda.synchronize()
+    prep._ws.clear()
+    ref_scale = float(y1.float().abs().max())
+    assert float((y.float() - y1.float()).abs().max()) <= 1e-2 * ref_scale
+    n0, n1 = 65536 - 256, n  # last whole tile and the 4 split tiles
+    sub = synth.GPTQCase("t", k, n1 - n0, 4, 128, False, c.qweight[:, n0:n1].contiguous(),
+                         c.qzeros[:, n0 // 8:n1 // 8].contiguous(), c.scales[:, n0:n1].contiguous(), None)
+    w = _oracle_w(sub, dtype)
+    xb = _np(x.cpu().view(torch.int16)).view(np.uint16) if dtype == "bf16" else _np(x.cpu())
+    bs = b[n0:n1].cpu()
+    bb = _np(bs.view(torch.int16)).view(np.uint16) if dtype == "bf16" else _np(bs)
+    ref = og.linear_ref(xb, w, dtype, bb)
+    r = _rel(_np(y[:, n0:n1].float()), ref)
+    assert r <= 1e-2, f"max rel err {r:.3e}"
