@@ -192,7 +192,7 @@ def _rotation(weight_bytes, ms, rotate_bytes=1 << 30):
     return max(1, min(32, -(-rotate_bytes // weight_bytes))) if min(ms) <= 64 else 1
 
 
-def report_configs(dev):
+def report_configs(dev, only=None):
     """BASELINE configs 0-4 at every listed M: µs per apply(), GB/s, TFLOP/s, binding roof."""
     import torch
 
@@ -203,6 +203,7 @@ def report_configs(dev):
             (1, synth.layer_cases(1), (1, 8, 32, 128), torch.float16),
             (2, synth.config_cases(2), (1, 16, 64, 256), torch.float16),
             (4, synth.config_cases(4), (2048, 4096, 8192), torch.bfloat16)]
+    plan = [p for p in plan if only is None or p[0] in only]
     for cfg, cases, ms, dt in plan:
         dname = "fp16" if dt == torch.float16 else "bf16"
         for c in cases:
@@ -222,7 +223,7 @@ def report_configs(dev):
             del preps, p0
             torch.cuda.empty_cache()
     # config 3: one DBF path and the two-path MDBF variant, per shape
-    for i, (name, k, n) in enumerate(synth.CONFIG3):
+    for i, (name, k, n) in enumerate(synth.CONFIG3 if only is None or 3 in only else []):
         cases = [synth.dbf_case(name, k, n, 1.0, seed=300 + 2 * i + j) for j in range(2)]
         ms = (1, 32, 512)
         copies = _rotation(sum(c.weight_bytes() for c in cases), ms)
@@ -331,6 +332,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config report (BASELINE configs 0-4 at every M)")
+    ap.add_argument("--configs-only", type=str, default=None,
+                    help="comma-separated BASELINE configs: print only their per-config report")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the M=2048 dequant-GEMM measurement (config 4 gate_up, bf16)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -352,6 +355,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
+        return
+    if args.configs_only is not None:
+        print(json.dumps({"configs": report_configs(dev, {int(c) for c in args.configs_only.split(",")})}))
         return
     if args.gemm_only:
         print(json.dumps(bench_gemm_large(2048, args.steps, args.warmup, dev)))

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 1
+#define OC_ABI_VERSION 2
 
 enum {
   OC_OK = 0,
@@ -140,13 +140,22 @@ typedef struct {
   int ld_in;
 } oc_sign_term;
 
+/* Device workspace bytes oc_sign_gemm needs for these terms at M rows (host only).  0 while M is
+ * below the large-M threshold (the GEMV path needs none); otherwise the pre-scaled inputs
+ * RNE(in * pre) of the terms that have a pre scale plus fp32 partial tiles (split tail, or one
+ * slot per term and tile when n_terms > 1). */
+size_t oc_sign_workspace_bytes(const oc_sign_term* terms, int n_terms, int M, int R);
+
 /* out[m, n] = sum over terms of the term above (+ bias[n]) for n < R, rounded once to act_dtype;
  * columns R <= n < fill_to are written as 0.  n_terms <= 4; all terms need the same unit size.
  * A DBF stage is one term (vllm_plugin.py:275-294: stage 1 pre=scaling0, post=scaling2; stage 2
  * post=scaling4), the P paths of MDBF stage 2 are P terms summed in one call
- * (mdbf_layer.py:338-344, :412-420).  Replaces DBFLinearMethod._apply_naive/_apply_gemlite. */
+ * (mdbf_layer.py:338-344, :412-420).  workspace: oc_sign_workspace_bytes() bytes of device memory
+ * (NULL when that is 0); no allocation, no memset, no host synchronisation.
+ * Replaces DBFLinearMethod._apply_naive/_apply_gemlite. */
 int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R, int act_dtype,
-                 const void* bias, void* out, int ld_out, int fill_to, void* stream);
+                 const void* bias, void* out, int ld_out, int fill_to, void* workspace,
+                 size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

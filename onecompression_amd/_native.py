@@ -36,10 +36,11 @@ SIGNATURES = {
     "oc_dbf_layout": (c_int, [c_int, c_int, c_size_t_p, c_int_p, c_int_p]),
     "oc_dbf_unpack_signs": (c_int, [P, c_int, c_int, P, P]),
     "oc_dbf_prepare": (c_int, [P, c_int, c_int, P, P]),
-    "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P]),
+    "oc_sign_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
+    "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, c_size_t, P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
 OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2
 ERR_NAMES = {-1: "INVALID", -2: "UNSUPPORTED", -3: "SHAPE", -4: "HIP", -5: "WORKSPACE", -6: "GIDX"}

@@ -19,6 +19,7 @@
 //     ((rt * NU + u) * 64 + l) * 4 * UK.
 #include <stdlib.h>
 
+#include "gemm_core.h"
 #include "oc_common.h"
 
 namespace {
@@ -324,8 +325,166 @@ extern "C" int oc_dbf_prepare(const uint8_t* bp, int R, int Kd, void* packed, vo
   return 0;
 }
 
+namespace {
+
+// ---------------------------------------------------------------------------
+// M >= kSignGemmMinM: the shared large-M GEMM core with the sign decoder.
+// A term with a pre scale first writes RNE(in * pre) (the reference's
+// `x * scaling0.to(x.dtype)`) to the workspace; the MFMA B operand is then the
+// exact +-1 pair.  One term: one k_gemm launch (+ fixup for a split tail).
+// Several terms: one launch per term, every tile written as an fp32 partial
+// (post-scaled) into its slot, then one fixup sums the slots and adds bias.
+// ---------------------------------------------------------------------------
+int sign_gemm_min_m() { return env_int("OC_SIGN_GEMM_MIN_M", 128); }
+
+int round8(int v) { return (v + 7) / 8 * 8; }
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+template <bool BF16>
+__global__ void k_prescale(const uint16_t* __restrict__ in, int ld_in, const uint16_t* __restrict__ pre, int Kd,
+                           int ldx, uint16_t* __restrict__ xs) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (k >= ldx) return;
+  uint16_t v = 0;
+  if (k < Kd) {
+    const uint16_t a = in[(size_t)m * ld_in + k], b = pre[k];
+    v = BF16 ? oc_f2bf(oc_bf2f(a) * oc_bf2f(b)) : oc_f2h(oc_h2f(a) * oc_h2f(b));
+  }
+  xs[(size_t)m * ldx + k] = v;
+}
+
+__global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int c1) {
+  const int c = c0 + threadIdx.x;
+  if (c < c1) out[(size_t)blockIdx.x * ld_out + c] = 0;
+}
+
+struct SignGemmPlan {
+  oc_gemm::GemmPlan gp;  // tiling of one term
+  size_t xs_off[kMaxTerms], part_off, bytes;
+};
+
+SignGemmPlan plan_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R) {
+  SignGemmPlan p;
+  const SignLayout L = make_sign_layout(R, terms[0].Kd);
+  // several terms are summed through partial slots: no K split inside a term
+  p.gp = oc_gemm::plan_gemm(M, L.RT * 16, L.K_pad, n_terms > 1 ? 1 : env_int("OC_GEMM_SPLIT", 0));
+  size_t off = 0;
+  for (int i = 0; i < n_terms; ++i) {
+    p.xs_off[i] = off;
+    if (terms[i].pre) off += align256((size_t)M * round8(terms[i].Kd) * 2);
+  }
+  p.part_off = off;
+  if (n_terms > 1)
+    off += (size_t)p.gp.MB * p.gp.NB * n_terms * oc_gemm::kGemmBM * oc_gemm::kGemmBN * 4;
+  else
+    off += align256(p.gp.part_bytes);
+  p.bytes = off;
+  return p;
+}
+
+template <bool BF16>
+void launch_sign_gemm_term(const oc_gemm::GemmArgs& g, int grid, hipStream_t st) {
+  hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16>), dim3(grid), dim3(256), 2 * oc_gemm::kGemmXBuf, st, g);
+}
+
+int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool bf16, const void* bias,
+                    void* out, int ld_out, int fill_to, void* workspace, size_t ws_bytes, hipStream_t st) {
+  const SignGemmPlan p = plan_sign_gemm(terms, n_terms, M, R);
+  OC_REQUIRE(ws_bytes >= p.bytes && (p.bytes == 0 || workspace), OC_ERR_WORKSPACE,
+             "workspace of %zu bytes is smaller than the %zu required", ws_bytes, p.bytes);
+  uint8_t* ws = (uint8_t*)workspace;
+  for (int i = 0; i < n_terms; ++i) {
+    const oc_sign_term& T = terms[i];
+    const SignLayout L = make_sign_layout(R, T.Kd);
+    oc_gemm::GemmArgs g = {};
+    g.w = (const uint8_t*)T.packed;
+    g.post = (const uint16_t*)T.post;
+    g.y = (uint16_t*)out;
+    g.part = (float*)(ws + p.part_off);
+    g.M = M;
+    g.K = T.Kd;
+    g.N = R;
+    g.N_pad = L.RT * 16;
+    g.NT_total = L.RT;
+    g.NU = L.NU;
+    g.G = 1;
+    g.gs = L.K_pad;
+    g.gshift = -1;
+    g.NKB = L.K_pad / 128;
+    g.MB = p.gp.MB;
+    g.NB = p.gp.NB;
+    g.ldy = ld_out;
+    g.uk_shift = L.UK == 4 ? 2 : (L.UK == 2 ? 1 : 0);
+    if (T.pre) {
+      const int ldx = round8(T.Kd);
+      uint16_t* xs = (uint16_t*)(ws + p.xs_off[i]);
+      const dim3 pg((ldx + 255) / 256, M);
+      if (bf16)
+        hipLaunchKernelGGL(k_prescale<true>, pg, dim3(256), 0, st, (const uint16_t*)T.in, T.ld_in,
+                           (const uint16_t*)T.pre, T.Kd, ldx, xs);
+      else
+        hipLaunchKernelGGL(k_prescale<false>, pg, dim3(256), 0, st, (const uint16_t*)T.in, T.ld_in,
+                           (const uint16_t*)T.pre, T.Kd, ldx, xs);
+      OC_HIP(hipGetLastError());
+      g.x = xs;
+      g.ldx = ldx;
+    } else {
+      g.x = (const uint16_t*)T.in;
+      g.ldx = T.ld_in;
+    }
+    if (n_terms == 1) {
+      g.bias = (const uint16_t*)bias;
+      g.tiles_main = p.gp.tiles_main;
+      g.S = p.gp.S;
+      g.kper = p.gp.kper;
+      g.pstride = p.gp.S;
+      g.poff = 0;
+    } else {  // every tile is one partial slot of this term
+      g.bias = nullptr;
+      g.tiles_main = 0;
+      g.S = 1;
+      g.kper = g.NKB;
+      g.pstride = n_terms;
+      g.poff = i;
+    }
+    const int grid = n_terms == 1 ? p.gp.tiles_main + p.gp.split_tiles * p.gp.S : p.gp.MB * p.gp.NB;
+    if (bf16) launch_sign_gemm_term<true>(g, grid, st);
+    else launch_sign_gemm_term<false>(g, grid, st);
+    OC_HIP(hipGetLastError());
+    if (i == n_terms - 1) {
+      const int fix_tiles = n_terms == 1 ? p.gp.split_tiles : p.gp.MB * p.gp.NB;
+      if (fix_tiles > 0) {
+        g.bias = (const uint16_t*)bias;
+        g.tiles_main = n_terms == 1 ? p.gp.tiles_main : 0;
+        g.pstride = n_terms == 1 ? p.gp.S : n_terms;
+        const dim3 fg(oc_gemm::kGemmBM * oc_gemm::kGemmBN / 256, fix_tiles);
+        if (bf16) hipLaunchKernelGGL(oc_gemm::k_gemm_fixup<true>, fg, dim3(256), 0, st, g);
+        else hipLaunchKernelGGL(oc_gemm::k_gemm_fixup<false>, fg, dim3(256), 0, st, g);
+        OC_HIP(hipGetLastError());
+      }
+    }
+  }
+  if (fill_to > R) {
+    hipLaunchKernelGGL(k_zero_cols, dim3(M), dim3(64), 0, st, (uint16_t*)out, ld_out, R, fill_to);
+    OC_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" size_t oc_sign_workspace_bytes(const oc_sign_term* terms, int n_terms, int M, int R) {
+  if (!terms || n_terms < 1 || n_terms > kMaxTerms || M < sign_gemm_min_m() || R <= 0) return 0;
+  for (int i = 0; i < n_terms; ++i)
+    if (terms[i].Kd <= 0) return 0;
+  return plan_sign_gemm(terms, n_terms, M, R).bytes;
+}
+
 extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R, int act_dtype,
-                            const void* bias, void* out, int ld_out, int fill_to, void* stream) {
+                            const void* bias, void* out, int ld_out, int fill_to, void* workspace,
+                            size_t ws_bytes, void* stream) {
   OC_REQUIRE(terms && out, OC_ERR_INVALID, "null pointer");
   OC_REQUIRE(n_terms >= 1 && n_terms <= kMaxTerms, OC_ERR_UNSUPPORTED, "n_terms=%d must be 1..%d", n_terms,
              kMaxTerms);
@@ -357,6 +516,9 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
     start += L.NU;
   }
   for (int i = n_terms; i <= kMaxTerms; ++i) a.unit_start[i] = start;
+  if (M >= sign_gemm_min_m())
+    return sign_gemm_large(terms, n_terms, M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to,
+                           workspace, ws_bytes, (hipStream_t)stream);
   a.n_terms = n_terms;
   a.bias = (const uint16_t*)bias;
   a.R = R;

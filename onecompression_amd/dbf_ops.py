@@ -97,8 +97,10 @@ def sign_gemm(terms, M: int, R: int, dtype: torch.dtype, out: torch.Tensor, ld_o
         arr[i] = OcSignTerm(f.packed.data_ptr(), x.data_ptr(), 0 if pre is None else pre.data_ptr(),
                             0 if post is None else post.data_ptr(), f.Kd, x.stride(0))
         keep.append(x)
+    nbytes = N.load().oc_sign_workspace_bytes(arr, len(terms), M, R)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=out.device) if nbytes else None
     N.call("oc_sign_gemm", arr, len(terms), M, R, _DT[dtype], _ptr(bias), _ptr(out), ld_out,
-           fill_to, _stream(out.device))
+           fill_to, _ptr(ws), nbytes, _stream(out.device))
 
 
 def _ld(n: int) -> int:

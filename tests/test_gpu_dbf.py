@@ -56,7 +56,9 @@ def test_sign_matmul_known_answer(dev):
 
 
 @pytest.mark.parametrize("k,n,m", [(256, 192, 1), (256, 192, 3), (640, 256, 16), (512, 384, 37),
-                                   (4096, 14336, 1), (14336, 4096, 1), (4096, 14336, 32)])
+                                   (4096, 14336, 1), (14336, 4096, 1), (4096, 14336, 32),
+                                   # M >= 128: the large-M GEMM core with the sign decoder
+                                   (512, 384, 130), (640, 1000, 300), (4096, 14336, 160)])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_dbf_forward(dev, k, n, m, dtype):
     if dtype == "bf16" and k * n > 4096 * 4096:
@@ -133,7 +135,8 @@ def _mdbf_path(n, m, r, l, seed):
                 A_amp=amp(n, l), B_amp=amp(m, l), Q_U_amp=amp(r, l), Q_V_amp=amp(r, l))
 
 
-@pytest.mark.parametrize("P,l,m_rows", [(2, 1, 1), (2, 1, 32), (1, 2, 4), (2, 2, 1)])
+@pytest.mark.parametrize("P,l,m_rows", [(2, 1, 1), (2, 1, 32), (1, 2, 4), (2, 2, 1),
+                                        (2, 1, 200), (1, 2, 150), (2, 2, 140)])  # large-M: partial slots
 def test_mdbf_forward(dev, P, l, m_rows):
     n, m = 384, 256
     r = od.mid_features(1.0, m, n)
@@ -145,3 +148,28 @@ def test_mdbf_forward(dev, P, l, m_rows):
     y = dbf_ops.mdbf_forward(x.to(dev), preps).float().cpu().numpy()
     ref = od.mdbf_forward(x.numpy(), paths)
     assert _rel(y, ref) <= 1e-2, _rel(y, ref)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_sign_gemm_large_fill_and_bias(dev, dtype):
+    """Large-M sign matmul: pre/post scales, bias, zero columns R..fill_to, ld_out > fill_to."""
+    m, kd, R, fill_to, ld_out = 140, 300, 37, 40, 48
+    rng = np.random.default_rng(7)
+    signs = rng.choice([-1, 1], size=(R, kd))
+    f = dbf_ops.sign_prepare(_t(od.pack_binary(signs), dev), R, kd)
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    x = torch.zeros((m, 304), dtype=td)
+    x[:, :kd] = torch.randn(m, kd, generator=torch.Generator().manual_seed(1)).to(td)
+    pre = torch.zeros(304, dtype=td)
+    pre[:kd] = torch.rand(kd, generator=torch.Generator().manual_seed(2)).to(td) + 0.5
+    post = (torch.rand(R, generator=torch.Generator().manual_seed(3)) + 0.5).to(td)
+    bias = (torch.randn(R, generator=torch.Generator().manual_seed(4)) * 0.1).to(td)
+    out = torch.full((m, ld_out), 7.0, dtype=td, device=dev)
+    dbf_ops.sign_gemm([(f, x.to(dev), pre.to(dev), post.to(dev))], m, R, td, out, ld_out, fill_to=fill_to,
+                      bias=bias.to(dev))
+    o = out.float().cpu()
+    xs = (x[:, :kd].float() * pre[:kd].float()).to(td).float()  # RNE(x * pre) as the reference
+    ref = (xs @ torch.from_numpy(signs).float().t()) * post.float() + bias.float()
+    assert _rel(o[:, :R].numpy(), ref.numpy()) <= 1e-2
+    assert torch.all(o[:, R:fill_to] == 0)
+    assert torch.all(o[:, fill_to:] == 7.0)
