@@ -157,6 +157,26 @@ int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R, int act_d
                  const void* bias, void* out, int ld_out, int fill_to, void* workspace,
                  size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- online Hadamard ---------- */
+
+/* Block order K the reference picks for dimension n (host only): the largest listed order dividing
+ * n with n / K a power of two, 1 for a power of two, 0 when the reference would assert.
+ * Replaces get_hadK's search, onecomp/pre_process/hadamard_utils.py:79-175. */
+int oc_hadamard_order(int n);
+
+/* Fill out[K * K] (int8 +-1, row-major) with the order-K block (host only).  K = 1, or one of
+ * 12, 20, 28, 36, 40, 44, 60, 68, 76, 108, 140 (built by construction; 52, 100, 156, 172 return
+ * OC_ERR_UNSUPPORTED).  Replaces get_had<K>, hadamard_utils.py:211-120444. */
+int oc_hadamard_block(int K, int8_t* out);
+
+/* y[m, :] = (H_K (x) H_L) x[m, :] / sqrt(n) with n = K * L, L a power of two, n <= 32768;
+ * hadk: device int8 [K * K] from oc_hadamard_block (NULL when K = 1).  fp32 internally, one
+ * rounding to act_dtype; y may alias x when ld_y == ld_x.  One kernel on `stream`.
+ * Replaces matmul_hadU_cuda (hadamard_utils.py:178-199) as applied to the down_proj input by
+ * apply_online_hadamard / RotatedLinearMethod (vllm_plugins/utils/rotation.py:100-112, 146-228). */
+int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* hadk, int K, int act_dtype,
+                void* y, int ld_y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
-from typing import Optional
+from typing import Dict, Optional
 
 import torch
 
@@ -162,3 +162,47 @@ def gptq_gemm(x: torch.Tensor, prep: PreparedGPTQ, bias: Optional[torch.Tensor] 
            prep.bits, prep.group_size, _DT[x.dtype], _ptr(bias), _ptr(out), _ptr(ws), ws_bytes,
            _stream(dev))
     return out.reshape(*lead, n)
+
+
+# ---------------------------------------------------------------------------------- Hadamard
+
+_HAD_BLOCKS: Dict = {}
+
+
+def hadamard_order(n: int) -> int:
+    """Block order the reference picks for n (hadamard_utils.py:79-175); raises where it asserts."""
+    k = N.load().oc_hadamard_order(n)
+    if k == 0:
+        raise ValueError(f"no Hadamard decomposition n = K * 2^m for n={n}")
+    return k
+
+
+def hadamard_block(k: int, device) -> Optional[torch.Tensor]:
+    """Device int8 [k, k] block (cached per device), None for k = 1."""
+    if k == 1:
+        return None
+    key = (k, str(device))
+    t = _HAD_BLOCKS.get(key)
+    if t is None:
+        host = (ctypes.c_int8 * (k * k))()
+        N.call("oc_hadamard_block", k, host)
+        t = torch.tensor(list(host), dtype=torch.int8).view(k, k).to(device)
+        _HAD_BLOCKS[key] = t
+    return t
+
+
+def hadamard(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Online Hadamard of the last axis: (H_K (x) H_L) x / sqrt(n), fp32 inside, one rounding."""
+    if x.dtype not in _DT:
+        raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
+    n = x.shape[-1]
+    k = hadamard_order(n)
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if out is None:
+        out = torch.empty_like(x2)
+    blk = hadamard_block(k, x.device)
+    N.call("oc_hadamard", _ptr(x2), x2.shape[0], n, x2.stride(0), _ptr(blk), k, _DT[x.dtype], _ptr(out),
+           out.stride(0), _stream(x.device))
+    return out.reshape(x.shape)

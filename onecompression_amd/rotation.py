@@ -1,10 +1,19 @@
-"""Rotation metadata of rotated (SpinQuant/OstQuant-preprocessed) checkpoints.
+"""Rotated (SpinQuant/OstQuant-preprocessed) checkpoints: metadata and the online Hadamard.
 
-Mirrors vllm_plugins/utils/rotation.py:75-97 (``RotationMetadata``) and the
-target predicate of onecomp/pre_process/rotation_utils.py:125-136.  A rotated
-checkpoint needs an online Hadamard transform of the ``mlp.down_proj`` input
-(vllm_plugins/utils/rotation.py:146-261).  That transform is not built here
-yet, so asking for it raises instead of silently computing wrong outputs.
+Mirrors vllm_plugins/utils/rotation.py:
+- ``RotationMetadata`` (:75-97) and the target predicate of
+  onecomp/pre_process/rotation_utils.py:125-136;
+- ``RotatedLinearMethod`` (:146-228): wraps a layer's linear method and
+  transforms the ``mlp.down_proj`` input online, y = (H_K (x) H_L) x / sqrt(n),
+  through a forward pre-hook installed at create_weights /
+  process_weights_after_loading, as the reference does for tp = 1.  The
+  transform is one HIP kernel (``ops.hadamard``); it computes in fp32 and
+  rounds once, which is the reference's ``fp32_had=True`` arithmetic (with
+  ``fp32_had=False`` the reference rounds in the activation dtype between
+  steps, within a few units in the last place of this result);
+- ``maybe_wrap_rotation_method`` (:242-261).
+Tensor parallelism > 1 needs an all-gather of the input first (:179-195);
+this one-GPU build raises for it.
 """
 
 from __future__ import annotations
@@ -34,10 +43,69 @@ class RotationMetadata:
         return self.rotated and is_online_hadamard_target(prefix)
 
 
+def apply_online_hadamard(x, *, fp32_had: bool = False, cache_owner: Any = None):
+    """Online Hadamard of the last axis (rotation.py:100-112); the block order is cached on the owner."""
+    from . import ops
+
+    del fp32_had  # always fp32 inside, one rounding (see the module docstring)
+    if cache_owner is not None:
+        cached = getattr(cache_owner, "_onecomp_hadamard_cache", None)
+        if cached is None or cached[0] != x.shape[-1]:
+            setattr(cache_owner, "_onecomp_hadamard_cache", (x.shape[-1], ops.hadamard_order(x.shape[-1])))
+    return ops.hadamard(x)
+
+
+def make_hadamard_forward_pre_hook(*, fp32_had: bool):
+    """Layer pre-hook that transforms the first positional input (rotation.py:115-125)."""
+
+    def hook(layer, inputs):
+        if not inputs:
+            return inputs
+        return (apply_online_hadamard(inputs[0], fp32_had=fp32_had, cache_owner=layer), *inputs[1:])
+
+    return hook
+
+
+class RotatedLinearMethod:
+    """Linear-method wrapper that transforms the layer input online (rotation.py:146-228)."""
+
+    def __init__(self, base_method, *, fp32_had: bool):
+        self.base_method = base_method
+        self.fp32_had = fp32_had
+
+    def _check_tp(self, layer) -> None:
+        tp_size = getattr(layer, "tp_size", 1) or 1
+        if getattr(layer, "input_is_parallel", False) and tp_size > 1:
+            raise NotImplementedError("tensor-parallel rotated down_proj needs an all-gather before the "
+                                      "Hadamard; this build runs one GPU")
+
+    def _ensure_hadamard_pre_hook(self, layer) -> None:
+        self._check_tp(layer)
+        if getattr(layer, "_onecomp_hadamard_prehook_installed", False):
+            return
+        handle = layer.register_forward_pre_hook(make_hadamard_forward_pre_hook(fp32_had=self.fp32_had))
+        setattr(layer, "_onecomp_hadamard_prehook_installed", True)
+        setattr(layer, "_onecomp_hadamard_prehook_handle", handle)
+
+    def create_weights(self, layer, *weight_args, **extra_weight_attrs):
+        self._ensure_hadamard_pre_hook(layer)
+        return self.base_method.create_weights(layer, *weight_args, **extra_weight_attrs)
+
+    def process_weights_after_loading(self, layer) -> None:
+        self._ensure_hadamard_pre_hook(layer)
+        process = getattr(self.base_method, "process_weights_after_loading", None)
+        if process is not None:
+            process(layer)
+
+    def apply(self, layer, x, bias=None, *args, **kwargs):
+        return self.base_method.apply(layer, x, bias, *args, **kwargs)
+
+    def __getattr__(self, name):  # expose the wrapped method's extras (e.g. quant_config)
+        return getattr(self.base_method, name)
+
+
 def maybe_wrap_rotation_method(method, *, prefix: str, metadata: RotationMetadata):
-    """Return ``method`` unchanged, or raise for layers that need the online Hadamard."""
+    """``method`` unchanged, or wrapped with the online Hadamard for rotated down_proj layers."""
     if not metadata.requires_hadamard(prefix):
         return method
-    raise NotImplementedError(
-        f"{prefix}: rotated checkpoints need the online Hadamard transform of the down_proj "
-        "input, which onecomp-amd does not implement yet")
+    return RotatedLinearMethod(method, fp32_had=metadata.fp32_had)

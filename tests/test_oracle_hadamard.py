@@ -1,0 +1,98 @@
+"""The online-Hadamard oracle and the C ABI's host-side block construction."""
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import hadamard as oh
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "hadamard_digests.json")
+BUILT = [K for K, how, _ in oh.ORDERS if how is not None]
+
+
+def _digest(H):
+    return hashlib.sha256(np.ascontiguousarray(np.asarray(H, dtype=np.int8)).tobytes()).hexdigest()
+
+
+@pytest.mark.parametrize("K", BUILT)
+def test_blocks_match_reference_tables(K):
+    """The constructions reproduce get_had<K> of hadamard_utils.py bit for bit (digests of the tables)."""
+    with open(GOLDEN) as f:
+        digests = json.load(f)["digests"]
+    H = oh.hadamard_block(K)
+    assert H.shape == (K, K)
+    assert np.array_equal(H @ H.T, K * np.eye(K, dtype=np.int64))
+    assert _digest(H) == digests[str(K)]
+
+
+def test_planted_mistake_is_caught():
+    """Jacobsthal sign flipped (chi(b - a) instead of chi(a - b)): still Hadamard, wrong digest."""
+    with open(GOLDEN) as f:
+        digests = json.load(f)["digests"]
+    chi = oh._chi(11)
+    a = np.arange(11)
+    S = np.zeros((12, 12), dtype=np.int64)
+    S[0, 1:], S[1:, 0] = -1, 1
+    S[1:, 1:] = chi[(a[None, :] - a[:, None]) % 11]
+    H = S + np.eye(12, dtype=np.int64)
+    assert np.array_equal(H @ H.T, 12 * np.eye(12, dtype=np.int64))
+    assert _digest(H) != digests["12"]
+
+
+@pytest.mark.parametrize("K", [52, 100, 156, 172])
+def test_unbuilt_orders_raise(K):
+    with pytest.raises(NotImplementedError):
+        oh.hadamard_block(K)
+
+
+def test_pick_order():
+    assert oh.pick_order(14336) == 28      # Llama-3-8B intermediate
+    assert oh.pick_order(12288) == 12      # Qwen3-8B intermediate
+    assert oh.pick_order(17408) == 68      # Qwen3-14B intermediate
+    assert oh.pick_order(11008) == 172     # Llama-2-7B intermediate
+    assert oh.pick_order(4096) == 1
+    for bad in (3 * 28 * 8, 105, 1000):
+        with pytest.raises(ValueError):
+            oh.pick_order(bad)
+
+
+def test_fwht_closed_form():
+    n = 64
+    i = np.arange(n)
+    sylvester = (-1.0) ** np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :])
+    assert np.array_equal(oh.fwht(np.eye(n)), sylvester)
+    assert np.array_equal(oh.fwht(np.eye(n)[0]), np.ones(n))
+
+
+@pytest.mark.parametrize("n", [16, 24, 56, 80])
+def test_online_hadamard_is_the_normalised_kronecker_product(n):
+    T = oh.online_hadamard(np.eye(n))  # row m = transform of e_m
+    K = oh.pick_order(n)
+    L = n // K
+    i = np.arange(L)
+    HL = (-1.0) ** np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :])
+    expect = np.kron(oh.hadamard_block(K).astype(np.float64), HL) / np.sqrt(n)
+    assert np.allclose(T, expect.T, atol=1e-12)
+    assert np.allclose(T @ T.T, np.eye(n), atol=1e-12)
+
+
+def test_c_abi_blocks_and_orders_match_oracle():
+    """Host-only entry points of the library (no GPU needed)."""
+    import ctypes
+
+    from onecompression_amd import _native as N
+
+    lib = N.load()
+    for K in BUILT + [1]:
+        buf = (ctypes.c_int8 * (K * K))()
+        assert lib.oc_hadamard_block(K, buf) == 0
+        assert np.array_equal(np.array(list(buf), dtype=np.int64).reshape(K, K), oh.hadamard_block(K))
+    for K in (52, 100, 156, 172):
+        buf = (ctypes.c_int8 * (K * K))()
+        assert lib.oc_hadamard_block(K, buf) == N.OC_ERR_UNSUPPORTED
+    for n in (14336, 12288, 17408, 11008, 4096, 640):
+        assert lib.oc_hadamard_order(n) == oh.pick_order(n)
+    assert lib.oc_hadamard_order(1000) == 0

@@ -103,11 +103,32 @@ def test_attn_alias():
     assert MU.lookup_module_config(qb, 0, "attn.o_proj")["bits"] == 4
 
 
-def test_rotated_down_proj_is_refused():
-    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": QB, "rotated": True})
-    with pytest.raises(NotImplementedError, match="Hadamard"):
-        cfg.get_quant_method(_layer(), "model.layers.0.mlp.down_proj")
+def test_rotated_down_proj_is_wrapped():
+    """rotation.py:242-261: only mlp.down_proj of a rotated checkpoint gets the online Hadamard."""
+    from onecompression_amd import rotation as ROT
+
+    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": QB, "rotated": True, "fp32_had": True})
+    m = cfg.get_quant_method(_layer(), "model.layers.0.mlp.down_proj")
+    assert isinstance(m, ROT.RotatedLinearMethod) and isinstance(m.base_method, G.GPTQLinearMethod)
+    assert m.fp32_had
     assert isinstance(cfg.get_quant_method(_layer(), "model.layers.0.mlp.up_proj"), G.GPTQLinearMethod)
+    plain = G.MixedGPTQConfig.from_config({"quantization_bits": QB})
+    assert isinstance(plain.get_quant_method(_layer(), "model.layers.0.mlp.down_proj"), G.GPTQLinearMethod)
+
+
+def test_rotated_wrapper_installs_one_pre_hook():
+    from onecompression_amd import rotation as ROT
+
+    base = G.GPTQLinearMethod(G.GPTQLayerConfig(4, 128, False, False, "gptq"))
+    m = ROT.RotatedLinearMethod(base, fp32_had=False)
+    layer = torch.nn.Module()
+    m.create_weights(layer, 256, [64], 256, 64, torch.float16)
+    m.create_weights(layer, 256, [64], 256, 64, torch.float16)
+    assert layer._onecomp_hadamard_prehook_installed and len(layer._forward_pre_hooks) == 1
+    tp = torch.nn.Module()
+    tp.tp_size, tp.input_is_parallel = 2, True
+    with pytest.raises(NotImplementedError, match="all-gather"):
+        m.create_weights(tp, 256, [64], 256, 64, torch.float16)
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
