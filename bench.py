@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -222,6 +223,20 @@ def report_configs(dev, only=None):
                                   _gptq_bytes(c, m), 2.0 * m * c.in_features * c.out_features, us, dname))
             del preps, p0
             torch.cuda.empty_cache()
+    # online Hadamard of a rotated down_proj input (configs 1, 2, 4 intermediate sizes)
+    if only is None or only & {1, 2, 4}:
+        for cfg, n_dim, dt, ms in ((1, 14336, torch.float16, (1, 128)), (2, 12288, torch.float16, (1, 256)),
+                                   (4, 17408, torch.bfloat16, (2048,))):
+            if only is not None and cfg not in only:
+                continue
+            for m in ms:
+                x = synth.activations(m, n_dim, dt, seed=500 + m).to(dev)
+                y = torch.empty_like(x)
+                us = _time_graph(lambda i: ops.hadamard(x, out=y), 1, 64 if m <= 256 else 16)
+                k_blk = ops.hadamard_order(n_dim)
+                fl = 2.0 * m * n_dim * (k_blk + math.log2(n_dim // k_blk))
+                out.append(_entry(cfg, f"hadamard n={n_dim} (K={k_blk})", n_dim, n_dim, m, 0, 4 * m * n_dim, fl, us,
+                                  "fp16" if dt == torch.float16 else "bf16"))
     # config 3: one DBF path and the two-path MDBF variant, per shape
     for i, (name, k, n) in enumerate(synth.CONFIG3 if only is None or 3 in only else []):
         cases = [synth.dbf_case(name, k, n, 1.0, seed=300 + 2 * i + j) for j in range(2)]
@@ -313,6 +328,43 @@ def cpu_baseline(cases, m, budget_s=20.0, min_runs=3, max_runs=10, warmup=1):
             "sample": f"{len(runs)} full step(s) after {warmup} warmup of the same workload "
                       f"({len(cases)} layers, M={m}); numpy unpack + v1 restore + fp32 dequant, then "
                       f"torch.matmul fp32 on {threads} threads"}
+
+
+def cpu_baseline_dbf(m, runs=10, warmup=2):
+    """DoubleBinaryLinear.forward restated on the host (dbf_layer.py:251-268): unpack the two sign
+    factors (oracle), then x*s0 -> @S2^T -> *s2 -> @S1^T -> *s4 as fp32 torch matmuls; config 3
+    up_proj shape, one path."""
+    import numpy as np
+    import torch
+
+    from oracle import dbf as od
+    from onecompression_amd import synth
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    name, k, n = synth.CONFIG3[0]
+    c = synth.dbf_case(name, k, n, 1.0, seed=300)
+    x = torch.from_numpy(np.random.default_rng(1).normal(size=(m, k)).astype(np.float32))
+    s0, s2, s4 = (v.float() for v in (c.s0, c.s2, c.s4))
+
+    def run():
+        t0 = time.perf_counter()
+        S2 = torch.from_numpy(od.unpack_binary_factor(c.bp1.numpy(), (c.mid, k)).astype(np.float32))
+        S1 = torch.from_numpy(od.unpack_binary_factor(c.bp3.numpy(), (n, c.mid)).astype(np.float32))
+        t1 = time.perf_counter()
+        (((x * s0) @ S2.T) * s2 @ S1.T) * s4
+        return t1 - t0, time.perf_counter() - t1
+
+    for _ in range(warmup):
+        run()
+    rs = [run() for _ in range(runs)]
+    tot = statistics.median(a + b for a, b in rs)
+    nbytes = c.weight_bytes() + 2 * m * (k + n)
+    return {"value": nbytes / tot / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": _cpu_model(), "median_s": round(tot, 4),
+            "unpack_s": round(statistics.median(a for a, _ in rs), 4),
+            "matmul_s": round(statistics.median(b for _, b in rs), 4), "runs": runs, "warmup": warmup,
+            "sample": f"config 3 {name} {k}->{n} (r={c.mid}), one DBF path, M={m}: oracle unpack of both "
+                      f"sign factors + fp32 torch matmuls, {torch.get_num_threads()} threads"}
 
 
 def synth_config0():
@@ -411,6 +463,7 @@ def main():
         c0 = synth_config0()
         out["cpu_baseline_cfg0"] = {f"M={mm}": cpu_baseline(c0, mm, budget_s=15.0, min_runs=10, max_runs=10,
                                                              warmup=2) for mm in (1, 16)}
+        out["cpu_baseline_cfg3"] = {f"M={mm}": cpu_baseline_dbf(mm) for mm in (1, 32)}
     print(json.dumps(out))
 
 

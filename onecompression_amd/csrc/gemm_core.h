@@ -437,17 +437,7 @@ struct GemmPlan {
   size_t part_bytes;
 };
 
-inline int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-    cus[dev] = c;
-  }
-  return cus[dev];
-}
+inline int device_cus() { return oc_device_cus(); }
 
 // M rows, N_pad columns (multiple of 16), K_pad = 128 * k-blocks; split_env
 // forces the piece count (1 = never split, 0 = automatic).

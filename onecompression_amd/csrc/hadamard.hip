@@ -22,7 +22,13 @@
 // chi is the quadratic character mod q.  Orders 52, 100, 156 and 172 (Paley
 // over GF(25) / GF(49) and other constructions) are not built.
 //
-// The kernel computes in fp32 and rounds once to the activation dtype.
+// One kernel, one workgroup per row: the length-L transforms in fp32 in LDS,
+// then u = FWHT / sqrt(n) rounded to the activation dtype and the H_K block
+// mix on MFMA (fp32 accumulation, one more rounding).  With K = 1 the
+// transform is rounded once.  The reference's
+// default fp32_had=False path rounds three times (after the transform, after
+// the 1/sqrt(n) division, after the H_K product); its fp32_had=True path
+// rounds once, and differs from this one by the intermediate rounding.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -123,47 +129,306 @@ int pick_order(int n) {
   return is_pow2(n) ? 1 : 0;
 }
 
-constexpr int kHadMaxN = 32768;  // fp32 row in LDS: 128 KiB
+constexpr int kHadThreads = 1024;           // one workgroup per row
+constexpr size_t kHadMaxLds = 160 * 1024;   // LDS of one CU
 
-// One workgroup per row: FWHT of the K segments in LDS, then the K x K mix.
-// x and y may alias (in-place): each row is read completely into LDS before
-// any of it is written, and rows belong to distinct workgroups.
+typedef float had_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 had_bf2 __attribute__((ext_vector_type(2)));
+
 template <bool BF16>
-__global__ __launch_bounds__(1024) void k_hadamard(const uint16_t* x, int ld_x, int n, int K,
-                                                        const int8_t* __restrict__ hadk, float scale, uint16_t* y,
-                                                        int ld_y) {
-  extern __shared__ __align__(16) float u[];  // n floats, then K*K int8 of H_K
-  int8_t* hk = (int8_t*)(u + n);
-  const int row = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
-  const uint16_t* xr = x + (size_t)row * ld_x;
-  for (int i = tid; i < n; i += nt) u[i] = BF16 ? oc_bf2f(xr[i]) : oc_h2f(xr[i]);
-  if (K > 1)  // K = 1 passes no block (hadk may be NULL)
-    for (int i = tid; i < K * K; i += nt) hk[i] = hadk[i];
-  __syncthreads();
-  const int L = n / K;
-  for (int h = 1; h < L; h <<= 1) {
-    // n/2 butterflies: pair (i, i + h) with i in the lower half of its 2h block
-    for (int b = tid; b < n / 2; b += nt) {
-      const int i = (b / h) * 2 * h + (b % h);
-      const float p = u[i], q = u[i + h];
-      u[i] = p + q;
-      u[i + h] = p - q;
+__device__ __forceinline__ float had_in(uint16_t v) {
+  return BF16 ? oc_bf2f(v) : oc_h2f(v);
+}
+template <bool BF16>
+__device__ __forceinline__ uint16_t had_out(float v) {
+  return BF16 ? oc_f2bf(v) : oc_f2h(v);
+}
+// Two fp32 rounded (RNE) to one packed pair of the activation dtype.
+template <bool BF16>
+__device__ __forceinline__ uint32_t had_pair(float lo, float hi) {
+  if constexpr (BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(had_f2{lo, hi}, had_bf2));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(had_f2{lo, hi}, oc_half2));
+}
+
+// One radix-2^R pass: butterflies (a, b) -> (a + b, a - b) over bits
+// [b0, b0 + R) of the in-segment index, for every segment of the row at once
+// (the segment index sits above those bits, so one group never straddles two).
+// With b0 >= 6 the 64 lanes of a wave read 64 consecutive words per t: no
+// bank conflicts.
+template <int R>
+__device__ __forceinline__ void had_pass(float* f, int n, int b0) {
+  const int groups = n >> R;
+  for (int g = threadIdx.x; g < groups; g += kHadThreads) {
+    const int base = ((g >> b0) << (b0 + R)) | (g & ((1 << b0) - 1));
+    float v[1 << R];
+#pragma unroll
+    for (int t = 0; t < (1 << R); ++t) v[t] = f[base + (t << b0)];
+#pragma unroll
+    for (int s = 0; s < R; ++s)
+#pragma unroll
+      for (int t = 0; t < (1 << R); ++t)
+        if (!(t & (1 << s))) {
+          const float p = v[t], q = v[t | (1 << s)];
+          v[t] = p + q;
+          v[t | (1 << s)] = p - q;
+        }
+#pragma unroll
+    for (int t = 0; t < (1 << R); ++t) f[base + (t << b0)] = v[t];
+  }
+}
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() carries a release
+// fence that also waits for every outstanding global load, which would drain
+// the next row's prefetch at each barrier; the row's own global stores and the
+// prefetched loads need no ordering against other waves.
+__device__ __forceinline__ void had_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// v from lane (lane ^ (1 << s)), s = 0, 1, 2, by DPP: quad permutations for
+// xor 1 and 2; xor 4 as the half-row mirror (l -> 7 - l) then quad xor 3.
+template <int S>
+__device__ __forceinline__ float had_lane_xor(float v) {
+  const int b = __float_as_int(v);
+  if constexpr (S == 0) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+  if constexpr (S == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+  const int m = __builtin_amdgcn_mov_dpp(b, 0x141, 0xF, 0xF, false);
+  return __int_as_float(__builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, false));
+}
+
+// Butterflies over bits 0 .. min(lgL, 6) - 1 of 8 consecutive elements per
+// lane (element 8g + t, g = lane mod 64 + multiple of 64): bits 0-2 in
+// registers, bits 3-5 across lanes g ^ 1, g ^ 2, g ^ 4.  Every lane whose
+// elements are in the row has its partners in the row too (L >= 16 makes n
+// a multiple of 8 * (partner span)).
+__device__ __forceinline__ void had_first_bits(float (&v)[8], int lgL, int lane) {
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    if (b < lgL) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (!(t & (1 << b))) {
+          const float p = v[t], q = v[t | (1 << b)];
+          v[t] = p + q;
+          v[t | (1 << b)] = p - q;
+        }
     }
-    __syncthreads();
   }
-  uint16_t* yr = y + (size_t)row * ld_y;
-  if (K == 1) {
-    for (int i = tid; i < n; i += nt) yr[i] = BF16 ? oc_f2bf(u[i] * scale) : oc_f2h(u[i] * scale);
-    return;
+  if (lgL > 3) {
+    const float sg = (lane & 1) ? -1.f : 1.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = fmaf(sg, v[t], had_lane_xor<0>(v[t]));
   }
-  for (int o = tid; o < n; o += nt) {
-    const int i = o / L, j = o - i * L;
-    const int8_t* hrow = hk + i * K;
-    float acc = 0.f;
-    for (int c = 0; c < K; ++c) acc += (float)hrow[c] * u[c * L + j];
-    acc *= scale;
-    yr[o] = BF16 ? oc_f2bf(acc) : oc_f2h(acc);
+  if (lgL > 4) {
+    const float sg = (lane & 2) ? -1.f : 1.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = fmaf(sg, v[t], had_lane_xor<1>(v[t]));
   }
+  if (lgL > 5) {
+    const float sg = (lane & 4) ? -1.f : 1.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = fmaf(sg, v[t], had_lane_xor<2>(v[t]));
+  }
+}
+
+// Four +-1 int8 of H_K (one 32-bit word) as two packed halves of +-1.0.
+template <bool BF16>
+__device__ __forceinline__ void had_signs(uint32_t w, uint32_t& p01, uint32_t& p23) {
+  constexpr uint32_t one2 = BF16 ? 0x3F803F80u : 0x3C003C00u;
+  p01 = one2 | ((w & 0x80u) << 8) | ((w & 0x8000u) << 16);
+  p23 = one2 | ((w >> 8) & 0x8000u) | (w & 0x80000000u);
+}
+
+// Eight row elements 8g .. 8g+7 (zero past n) as fp32.
+template <bool BF16>
+__device__ __forceinline__ void had_load8(const uint16_t* xr, int n, int g, bool vx, float (&v)[8]) {
+  if (vx) {
+    const oc_u4 w = *(const oc_u4*)(xr + 8 * g);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      v[2 * t] = had_in<BF16>((uint16_t)(w[t] & 0xFFFF));
+      v[2 * t + 1] = had_in<BF16>((uint16_t)(w[t] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = 8 * g + t < n ? had_in<BF16>(xr[8 * g + t]) : 0.f;
+  }
+}
+
+constexpr int kHadPre = 4;  // prefetched 16-byte words of the next row per thread (n <= 32768)
+
+// y[m] = (H_K (x) H_L) x[m] / sqrt(n); each workgroup takes rows
+// blockIdx.x, + gridDim.x, ... and prefetches its next row into registers
+// while it transforms the current one.  Per row:
+//  1. the row's elements, 8 consecutive per thread; bits 0-5 of the length-L
+//     transform in registers and across lanes; fp32 to LDS;
+//  2. radix passes over the remaining bits in LDS (fp32);
+//  3. K = 1: scale, round, store.  K > 1: per chunk of J columns j, write
+//     u^T[j][c] = round(u[c][j] / sqrt(n)) (zero for c >= K) to LDS and form
+//     y[i][j] = sum_c H[i][c] u[c][j] with 16x16x32 MFMA (A = H_K as exact
+//     +-1 halves, staged in LDS once; fp32 accumulate; one rounding).
+// A row is read whole before any of it is stored, so y may alias x.
+template <bool BF16>
+__global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int ld_x, int M, int n, int lgL, int K,
+                                                          const int8_t* __restrict__ hadk, int lgJ, float scale,
+                                                          bool vx, bool vy, bool vy4, uint16_t* y, int ld_y) {
+  extern __shared__ __align__(16) float fbuf[];  // n floats | H_K [KR][US] | u^T [J][US]
+  const int tid = threadIdx.x;
+  const int L = 1 << lgL;
+  const int G8 = (n + 7) / 8;
+  const int KP = (K + 31) & ~31, US = KP + 8;  // LDS rows of H_K and u^T: KP halves + 8 of padding
+  const int J = 1 << lgJ, lgCT = lgJ - 4, RT = (K + 15) / 16, KS = KP / 32;
+  uint16_t* hs = (uint16_t*)(fbuf + n);
+  uint16_t* ut = hs + RT * 16 * US;
+  const int lane = tid & 63, wave = tid >> 6, col = lane & 15, kq = lane >> 4;
+  const bool pre = vx && G8 <= kHadPre * kHadThreads;
+
+  if (K > 1) {
+    for (int q = tid; q < RT * 16 * (KP / 8); q += kHadThreads) {
+      const int i = q / (KP / 8), c0 = 8 * (q % (KP / 8));
+      uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+      if (i < K && c0 < K) had_signs<BF16>(*(const uint32_t*)(hadk + i * K + c0), a0, a1);
+      if (i < K && c0 + 4 < K) had_signs<BF16>(*(const uint32_t*)(hadk + i * K + c0 + 4), a2, a3);
+      *(oc_u4*)(hs + i * US + c0) = oc_u4{a0, a1, a2, a3};
+    }
+  }
+  oc_u4 nxt[kHadPre];
+  if (pre && blockIdx.x < M) {
+    const uint16_t* xr = x + (size_t)blockIdx.x * ld_x;
+#pragma unroll
+    for (int s = 0; s < kHadPre; ++s)
+      if (tid + s * kHadThreads < G8) nxt[s] = *(const oc_u4*)(xr + 8 * (tid + s * kHadThreads));
+  }
+
+  for (int row = blockIdx.x; row < M; row += gridDim.x) {
+    const uint16_t* xr = x + (size_t)row * ld_x;
+    uint16_t* yr = y + (size_t)row * ld_y;
+#pragma unroll
+    for (int s = 0; s < kHadPre; ++s) {
+      const int g = tid + s * kHadThreads;
+      if (!pre && s > 0) break;
+      for (int gg = g; gg < G8; gg += pre ? G8 : kHadThreads) {  // one pass when prefetched
+        float v[8];
+        if (pre) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            v[2 * t] = had_in<BF16>((uint16_t)(nxt[s][t] & 0xFFFF));
+            v[2 * t + 1] = had_in<BF16>((uint16_t)(nxt[s][t] >> 16));
+          }
+        } else {
+          had_load8<BF16>(xr, n, gg, vx, v);
+        }
+        had_first_bits(v, lgL, lane);
+        float* fp = fbuf + 8 * gg;
+        if (8 * gg + 8 <= n) {
+          *(oc_f4*)fp = oc_f4{v[0], v[1], v[2], v[3]};
+          *(oc_f4*)(fp + 4) = oc_f4{v[4], v[5], v[6], v[7]};
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            if (8 * gg + t < n) fp[t] = v[t];
+        }
+      }
+    }
+    had_sync();
+    // the next row's loads run under this row's LDS work
+    if (pre && row + (int)gridDim.x < M) {
+      const uint16_t* xn = x + (size_t)(row + gridDim.x) * ld_x;
+#pragma unroll
+      for (int s = 0; s < kHadPre; ++s)
+        if (tid + s * kHadThreads < G8) nxt[s] = *(const oc_u4*)(xn + 8 * (tid + s * kHadThreads));
+    }
+
+    // bits 6 and up in LDS, in passes of at most 4 bits
+    int b0 = 6;
+    while (b0 < lgL) {
+      const int rem = lgL - b0;
+      const int r = (rem + (rem + 3) / 4 - 1) / ((rem + 3) / 4);
+      switch (r) {
+        case 1: had_pass<1>(fbuf, n, b0); break;
+        case 2: had_pass<2>(fbuf, n, b0); break;
+        case 3: had_pass<3>(fbuf, n, b0); break;
+        default: had_pass<4>(fbuf, n, b0); break;
+      }
+      b0 += r;
+      had_sync();
+    }
+
+    if (K == 1) {
+      for (int g = tid; g < G8; g += kHadThreads) {
+        const float* fp = fbuf + 8 * g;
+        if (vy) {
+          const oc_f4 a = *(const oc_f4*)fp, b = *(const oc_f4*)(fp + 4);
+          oc_u4 w;
+          w[0] = had_out<BF16>(a[0] * scale) | ((uint32_t)had_out<BF16>(a[1] * scale) << 16);
+          w[1] = had_out<BF16>(a[2] * scale) | ((uint32_t)had_out<BF16>(a[3] * scale) << 16);
+          w[2] = had_out<BF16>(b[0] * scale) | ((uint32_t)had_out<BF16>(b[1] * scale) << 16);
+          w[3] = had_out<BF16>(b[2] * scale) | ((uint32_t)had_out<BF16>(b[3] * scale) << 16);
+          *(oc_u4*)(yr + 8 * g) = w;
+        } else {
+          for (int t = 0; t < 8; ++t)
+            if (8 * g + t < n) yr[8 * g + t] = had_out<BF16>(fp[t] * scale);
+        }
+      }
+    } else {
+      for (int j0 = 0; j0 < L; j0 += J) {
+        for (int q = tid; q < (J << 2) * (KP / 32); q += kHadThreads) {
+          const int jj = q & (J - 1), c0 = 8 * (q >> lgJ), j = j0 + jj;
+          const float* fc = fbuf + c0 * L + j;
+          float v[8];
+          if (c0 + 8 <= K && j < L) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = fc[t * L] * scale;
+          } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = (c0 + t < K && j < L) ? fc[t * L] * scale : 0.f;
+          }
+          *(oc_u4*)(ut + jj * US + c0) = oc_u4{had_pair<BF16>(v[0], v[1]), had_pair<BF16>(v[2], v[3]),
+                                               had_pair<BF16>(v[4], v[5]), had_pair<BF16>(v[6], v[7])};
+        }
+        had_sync();
+        // y^T = u^T H^T: A = u^T rows j, B = H_K rows i; lane (col, kq) ends
+        // with y[i = 16 it + col][j = 16 ct + 4 kq .. + 3], one 8-byte store.
+        for (int p = wave; p < (RT << lgCT); p += kHadThreads / 64) {
+          const int it = p >> lgCT, ct = p & ((1 << lgCT) - 1);
+          oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+          for (int ks = 0; ks < KS; ++ks) {
+            const int c0 = ks * 32 + 8 * kq;
+            const oc_u4 av = *(const oc_u4*)(ut + (ct * 16 + col) * US + c0);
+            const oc_u4 bv = *(const oc_u4*)(hs + (it * 16 + col) * US + c0);
+            acc = oc_mfma16<BF16>(av, bv, acc);
+          }
+          const int i = it * 16 + col, j = j0 + ct * 16 + 4 * kq;
+          if (i < K) {
+            uint16_t* yo = yr + (size_t)i * L + j;
+            if (vy4 && j + 3 < L) {
+              *(uint2*)yo = uint2{had_pair<BF16>(acc[0], acc[1]), had_pair<BF16>(acc[2], acc[3])};
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (j + r < L) yo[r] = had_out<BF16>(acc[r]);
+            }
+          }
+        }
+        had_sync();
+      }
+    }
+    if (K == 1) had_sync();  // fbuf is rewritten by the next row
+  }
+}
+
+// Dynamic LDS of k_hadamard for (n, K) with chunks of J columns.
+size_t had_lds_bytes(int n, int K, int J) {
+  size_t b = (size_t)n * 4;
+  if (K > 1) b += (size_t)(((K + 15) / 16) * 16 + J) * (((K + 31) & ~31) + 8) * 2;
+  return b;
+}
+
+// log2 of the widest chunk (a power of two, 16 .. max(L, 16)) that fits the
+// LDS; -1 if none does.
+int had_chunk_log2(int n, int K) {
+  int lg = 4;
+  while ((1 << (lg + 1)) <= n / K) ++lg;
+  while (lg >= 4 && had_lds_bytes(n, K, 1 << lg) > kHadMaxLds) --lg;
+  return lg >= 4 ? lg : -1;
 }
 
 }  // namespace
@@ -191,17 +456,28 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
              act_dtype);
   OC_REQUIRE(K >= 1 && n % K == 0 && is_pow2(n / K), OC_ERR_SHAPE, "n=%d is not K=%d times a power of two", n, K);
   OC_REQUIRE(K == 1 || hadk, OC_ERR_INVALID, "K=%d needs the K x K block", K);
-  OC_REQUIRE(n <= kHadMaxN, OC_ERR_UNSUPPORTED, "n=%d above the %d supported", n, kHadMaxN);
+  OC_REQUIRE(K == 1 || K % 4 == 0, OC_ERR_SHAPE, "Hadamard order K=%d is not a multiple of 4", K);
+  OC_REQUIRE(K == 1 || ((uintptr_t)hadk & 3) == 0, OC_ERR_INVALID, "the K x K block must be 4-byte aligned");
+  const int lgJ = K > 1 ? had_chunk_log2(n, K) : 4;
+  const size_t lds = had_lds_bytes(n, K, lgJ >= 4 ? 1 << lgJ : 16);
+  OC_REQUIRE(lds <= kHadMaxLds, OC_ERR_UNSUPPORTED, "n=%d (K=%d) needs %zu bytes of LDS, above the %zu of one CU",
+             n, K, lds, kHadMaxLds);
   if (M == 0) return 0;
-  const size_t lds = (size_t)n * 4 + (size_t)K * K;
+  int lgL = 0;
+  while ((1 << lgL) < n / K) ++lgL;
   const float scale = 1.0f / sqrtf((float)n);
+  const bool vx = n % 8 == 0 && ld_x % 8 == 0 && ((uintptr_t)x & 15) == 0;
+  const bool vy = n % 8 == 0 && ld_y % 8 == 0 && ((uintptr_t)y & 15) == 0;
+  const bool vy4 = (n / K) % 4 == 0 && ld_y % 4 == 0 && ((uintptr_t)y & 7) == 0;
+  const int per_cu = (int)(kHadMaxLds / lds) < 2 ? 1 : 2;
+  const int grid = M < oc_device_cus() * per_cu ? M : oc_device_cus() * per_cu;
   hipStream_t st = (hipStream_t)stream;
   if (act_dtype == OC_DTYPE_BF16)
-    hipLaunchKernelGGL(k_hadamard<true>, dim3(M), dim3(1024), lds, st, (const uint16_t*)x, ld_x, n, K, hadk,
-                       scale, (uint16_t*)y, ld_y);
+    hipLaunchKernelGGL(k_hadamard<true>, dim3(grid), dim3(kHadThreads), lds, st, (const uint16_t*)x, ld_x, M, n,
+                       lgL, K, hadk, lgJ, scale, vx, vy, vy4, (uint16_t*)y, ld_y);
   else
-    hipLaunchKernelGGL(k_hadamard<false>, dim3(M), dim3(1024), lds, st, (const uint16_t*)x, ld_x, n, K, hadk,
-                       scale, (uint16_t*)y, ld_y);
+    hipLaunchKernelGGL(k_hadamard<false>, dim3(grid), dim3(kHadThreads), lds, st, (const uint16_t*)x, ld_x, M, n,
+                       lgL, K, hadk, lgJ, scale, vx, vy, vy4, (uint16_t*)y, ld_y);
   OC_HIP(hipGetLastError());
   return 0;
 }

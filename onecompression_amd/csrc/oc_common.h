@@ -102,6 +102,19 @@ __device__ __forceinline__ uint32_t oc_opaque(uint32_t v) {
 // address.  Emits no instruction.
 __device__ __forceinline__ void oc_wave_lds_barrier() { asm volatile("" ::: "memory"); }
 
+// Compute units of the current device (cached per device; 256 if unknown).
+inline int oc_device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cus[dev] = c;
+  }
+  return cus[dev];
+}
+
 template <bool BF16>
 __device__ __forceinline__ oc_f4 oc_mfma16(oc_u4 a, oc_u4 b, oc_f4 c) {
   if constexpr (BF16) {

@@ -7,10 +7,12 @@ Mirrors vllm_plugins/utils/rotation.py:
   transforms the ``mlp.down_proj`` input online, y = (H_K (x) H_L) x / sqrt(n),
   through a forward pre-hook installed at create_weights /
   process_weights_after_loading, as the reference does for tp = 1.  The
-  transform is one HIP kernel (``ops.hadamard``); it computes in fp32 and
-  rounds once, which is the reference's ``fp32_had=True`` arithmetic (with
-  ``fp32_had=False`` the reference rounds in the activation dtype between
-  steps, within a few units in the last place of this result);
+  transform is ``ops.hadamard`` (two HIP launches: the length-L transforms in
+  fp32, rounded once to the activation dtype, then the K x K mix on MFMA with
+  fp32 accumulation and one more rounding).  The reference's default
+  ``fp32_had=False`` rounds three times (transform, 1/sqrt(n), H_K product);
+  ``fp32_had=True`` rounds once, and this result differs from it by the one
+  intermediate rounding;
 - ``maybe_wrap_rotation_method`` (:242-261).
 Tensor parallelism > 1 needs an all-gather of the input first (:179-195);
 this one-GPU build raises for it.
@@ -47,7 +49,7 @@ def apply_online_hadamard(x, *, fp32_had: bool = False, cache_owner: Any = None)
     """Online Hadamard of the last axis (rotation.py:100-112); the block order is cached on the owner."""
     from . import ops
 
-    del fp32_had  # always fp32 inside, one rounding (see the module docstring)
+    del fp32_had  # one arithmetic for both settings (see the module docstring)
     if cache_owner is not None:
         cached = getattr(cache_owner, "_onecomp_hadamard_cache", None)
         if cached is None or cached[0] != x.shape[-1]:
