@@ -86,6 +86,15 @@ __device__ __forceinline__ uint32_t bf16_pair_f32(float lo, float hi) {
 constexpr int kGemmBM = 256, kGemmBN = 256;
 constexpr size_t kGemmXBuf = (size_t)kGemmBM * 256;  // bytes of one x buffer (128 k of bf16 per row)
 
+// Tile height 64 MT rows (MT = 1, 2, 4; 256 columns always): each wave holds
+// NI = 2 MT m32-tiles of its 64 columns and loads XJ = 4 MT KB of each x block.
+template <int MT>
+struct GemmTile {
+  static_assert(MT == 1 || MT == 2 || MT == 4, "tile height 64, 128 or 256");
+  static constexpr int BM = 64 * MT, NI = 2 * MT, XJ = 4 * MT;
+  static constexpr size_t XBUF = (size_t)BM * 256;  // bytes of one x buffer
+};
+
 typedef __attribute__((address_space(3))) void* oc_lds_ptr;
 
 template <bool BF16>
@@ -135,12 +144,14 @@ __device__ __forceinline__ oc_u4 gemm_apply(oc_u4 pr, GemmDeq<BF16> d) {
 // Scheduling of one 16-MFMA step: the next step's LDS reads go out first (16
 // MFMAs before their use), then each MFMA is followed by a share of the next
 // step's dequantisation, so the matrix pipe never waits on a burst of VALU.
+template <int NI = 8>
 __device__ __forceinline__ void gemm_interleave() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the next step's 8 LDS reads first
+  constexpr int VPM = 24 / NI > 3 ? 24 / NI : 3;  // VALU per MFMA: the step's dequant spread evenly
+  __builtin_amdgcn_sched_group_barrier(0x100, NI, 0);  // the next step's NI LDS reads first
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+  for (int i = 0; i < 2 * NI; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);  // VALU
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -155,8 +166,10 @@ struct GemmLoads {
   static constexpr int n = 4 * per + (BITS == 1 ? 0 : 2 * (4 / CS));
 };
 
-template <int BITS, int CS, bool BF16>
+template <int BITS, int CS, bool BF16, int MT = 4>
 __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
+  using TL = GemmTile<MT>;
+  constexpr int NI = TL::NI;
   constexpr int NWB = KbWords<BITS>::n;
   constexpr int SPK = 4 / CS;  // meta words per n32-tile per k-block
   const int tid = threadIdx.x, lane = tid & 63;
@@ -171,7 +184,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   const int kb1 = piece ? min(kb0 + a.kper, a.NKB) : a.NKB;
   int mb, nb;
   gemm_tile(tile, a.MB, a.NB, mb, nb);
-  const int m0 = mb * kGemmBM;
+  const int m0 = mb * TL::BM;
   const int n0 = nb * kGemmBN + wave * 64;  // first column of this wave
   int nt[2], cl[2];
 #pragma unroll
@@ -185,25 +198,25 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 
   extern __shared__ __align__(16) uint8_t smem[];
 
-  // x tile loader: wave w, instruction j fills LDS bytes [(16w + j) KB, +1 KB):
-  // row 64w + 4j + lane/16, chunk position lane % 16.
-  const int rows_here = min(a.M - m0, kGemmBM);
+  // x tile loader: wave w, instruction j fills LDS bytes [(XJ w + j) KB, +1 KB):
+  // row 16 MT w + 4j + lane/16, chunk position lane % 16.
+  const int rows_here = min(a.M - m0, TL::BM);
   const int X2 = a.ldx * 2;  // bytes per x row
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (size_t)m0 * a.ldx), 0, rows_here * X2, 0x00020000);
-  const int xrow = 64 * wave + (lane >> 4);
+  const int xrow = 16 * MT * wave + (lane >> 4);
   int xcoff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) xcoff[j] = (r16 ^ ((4 * j + (lane >> 4)) & 15));
   auto load_x = [&](int kb, int buf) {
     const bool tail = (kb + 1) * 128 > a.K;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < TL::XJ; ++j) {
       const int c = xcoff[j & 3];
       int off = (xrow + 4 * j) * X2 + kb * 256 + c * 16;
       if (tail && kb * 128 + 8 * c >= a.K) off = 0x7FFFFFF0;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (oc_lds_ptr)(smem + buf * kGemmXBuf + (16 * wave + j) * 1024), 16,
-                                               off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (oc_lds_ptr)(smem + buf * TL::XBUF + (TL::XJ * wave + j) * 1024),
+                                               16, off, 0, 0, 0);
     }
   };
   // Packed words and scale/zero words of one k-block: loaded two k-blocks
@@ -264,9 +277,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 #pragma unroll
   for (int s = 0; s < 8; ++s) xa[s] = (lane & 31) * 256 + (((2 * s + h) ^ r16) * 16);
 
-  oc_f16v acc[8][2];
+  oc_f16v acc[NI][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
@@ -290,36 +303,36 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
       }
     }
   };
-  auto mma = [&](const oc_u4 (&A)[8], const oc_u4 (&B)[2]) {
+  auto mma = [&](const oc_u4 (&A)[NI], const oc_u4 (&B)[2]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int T = 0; T < 2; ++T) acc[i][T] = oc_mfma32<BF16>(A[i], B[T], acc[i][T]);
   };
   // One k-block: 8 steps of 16 k.  The A fragments and B operands of step
-  // s + 1 are read / dequantised while the 16 MFMAs of step s run; B of step 0
+  // s + 1 are read / dequantised while the 2 NI MFMAs of step s run; B of step 0
   // (B0 on entry) was prepared before the barrier that opened this k-block.
   auto compute = [&](int buf, const uint32_t (&wb)[2][2][NWB], const uint32_t (&mw)[2][SPK], oc_u4 (&B0)[2],
                      GemmDeq<BF16> (&dq)[2]) {
-    const uint8_t* xb = smem + buf * kGemmXBuf;
-    auto read_a = [&](int s, oc_u4 (&A)[8]) {
+    const uint8_t* xb = smem + buf * TL::XBUF;
+    auto read_a = [&](int s, oc_u4 (&A)[NI]) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) A[i] = *(const oc_u4*)(xb + xa[s] + i * 8192);
+      for (int i = 0; i < NI; ++i) A[i] = *(const oc_u4*)(xb + xa[s] + i * 8192);
     };
-    oc_u4 A0[8], A1[8], B1[2];
+    oc_u4 A0[NI], A1[NI], B1[2];
     read_a(0, A0);
 #pragma unroll
     for (int s = 0; s < 8; s += 2) {
       read_a(s + 1, A1);
       make_b(wb, mw, s + 1, B1, dq);
       mma(A0, B0);
-      gemm_interleave();
+      gemm_interleave<NI>();
       if (s + 2 < 8) {
         read_a(s + 2, A0);
         make_b(wb, mw, s + 2, B0, dq);
       }
       mma(A1, B1);
-      gemm_interleave();
+      gemm_interleave<NI>();
     }
   };
 
@@ -379,9 +392,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   if (piece) {
     // fp32 partial tile in register order [wave][i][T][r][lane]: 256-B stores
     const int slot = (pidx / a.S) * a.pstride + a.poff + pidx % a.S;
-    float* pp = a.part + (size_t)slot * (kGemmBM * kGemmBN) + wave * (8 * 2 * 16 * 64) + lane;
+    float* pp = a.part + (size_t)slot * (TL::BM * kGemmBN) + wave * (NI * 2 * 16 * 64) + lane;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int T = 0; T < 2; ++T)
 #pragma unroll
@@ -396,7 +409,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     float b = 0.f;
     if (a.bias) b = BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -409,27 +422,30 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 }
 
 // y for the K-split tiles: the pstride fp32 partial tiles summed in slot
-// order (deterministic) plus bias.  One thread per element of a 256 x 256 tile, in
-// the partials' register order.
-template <bool BF16>
+// order (deterministic) plus bias.  One thread per element of a BM x 256 tile,
+// in the partials' register order [wave][i][T][r][lane].
+template <bool BF16, int MT = 4>
 __global__ __launch_bounds__(256) void k_gemm_fixup(const GemmArgs a) {
+  using TL = GemmTile<MT>;
+  constexpr int LNI = MT == 1 ? 1 : (MT == 2 ? 2 : 3);  // log2 NI
   const int t = blockIdx.y;  // split tile
   const int e = blockIdx.x * 256 + threadIdx.x;
-  const int lane = e & 63, r = (e >> 6) & 15, T = (e >> 10) & 1, i = (e >> 11) & 7, wave = e >> 14;
+  const int lane = e & 63, r = (e >> 6) & 15, T = (e >> 10) & 1, i = (e >> 11) & (TL::NI - 1),
+            wave = e >> (11 + LNI);
   int mb, nb;
   gemm_tile(a.tiles_main + t, a.MB, a.NB, mb, nb);
-  const int m = mb * kGemmBM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+  const int m = mb * TL::BM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
   const int n = nb * kGemmBN + 64 * wave + 32 * T + (lane & 31);
   if (m >= a.M || n >= a.N) return;
-  const float* pp = a.part + (size_t)t * a.pstride * (kGemmBM * kGemmBN) + e;
+  const float* pp = a.part + (size_t)t * a.pstride * (TL::BM * kGemmBN) + e;
   float v = 0.f;
-  for (int s = 0; s < a.pstride; ++s) v += pp[(size_t)s * (kGemmBM * kGemmBN)];
+  for (int s = 0; s < a.pstride; ++s) v += pp[(size_t)s * (TL::BM * kGemmBN)];
   if (a.bias) v += BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
   a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(v) : oc_f2h(v);
 }
 
 
-// Large-M tiling: whole 256 x 256 tiles, except that a last round of tiles
+// Large-M tiling: whole 64 MT x 256 tiles, except that a last round of tiles
 // that would leave more than half of the CUs idle is cut along K into S
 // pieces (at least 4 k-blocks each) whose fp32 partials k_gemm_fixup sums.
 struct GemmPlan {
@@ -441,9 +457,10 @@ inline int device_cus() { return oc_device_cus(); }
 
 // M rows, N_pad columns (multiple of 16), K_pad = 128 * k-blocks; split_env
 // forces the piece count (1 = never split, 0 = automatic).
-inline GemmPlan plan_gemm(int M, int N_pad, int K_pad, int split_env) {
+inline GemmPlan plan_gemm(int M, int N_pad, int K_pad, int split_env, int MT = 4) {
   GemmPlan p;
-  p.MB = (M + kGemmBM - 1) / kGemmBM;
+  const int BM = 64 * MT;
+  p.MB = (M + BM - 1) / BM;
   p.NB = (N_pad + kGemmBN - 1) / kGemmBN;
   p.NKB = K_pad / 128;
   const int T = p.MB * p.NB, C = device_cus();
@@ -462,7 +479,7 @@ inline GemmPlan plan_gemm(int M, int N_pad, int K_pad, int split_env) {
     p.split_tiles = rem;
     p.tiles_main = T - rem;
   }
-  p.part_bytes = (size_t)p.split_tiles * p.S * kGemmBM * kGemmBN * 4;
+  p.part_bytes = (size_t)p.split_tiles * p.S * BM * kGemmBN * 4;
   return p;
 }
 

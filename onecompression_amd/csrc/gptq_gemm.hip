@@ -495,6 +495,30 @@ int launch_reduce(bool bf16, const float* partial, int S, int M, int N, int N_pa
 
 constexpr int kSkinnyMaxM = 64;
 
+// Tile height of the GEMM for M rows (64 MT rows, 256 columns): the tallest
+// that still leaves at least half as many tiles as CUs (measured: fewer,
+// taller tiles lose to more, shorter ones until the grid covers the GPU);
+// only 256-row tiles for groups that are not multiples of 128.
+int gemm_mt(int M, int N_pad, int gs) {
+  const int e = env_int("OC_GEMM_MT", 0);
+  if ((gs % 128) != 0) return 4;
+  if (e == 1 || e == 2 || e == 4) return e;
+  const int NB = (N_pad + 255) / 256, C = device_cus();
+  for (int mt = 4; mt > 1; mt /= 2)
+    if (((M + 64 * mt - 1) / (64 * mt)) * NB * 2 >= C) return mt;
+  return 1;
+}
+
+// The tiled GEMM from M = 33 (17 when there are 64 or more column tiles; 128
+// for groups that are not multiples of 128, which only have 256-row tiles);
+// the skinny kernel below that.  OC_GEMM_MIN_M overrides the threshold.
+bool use_gemm(int M, int N_pad, int gs) {
+  const int e = env_int("OC_GEMM_MIN_M", 0);
+  if (e > 0) return M >= e;
+  if ((gs % 128) != 0) return M >= 128;
+  return M > 32 || (M > kGemvMaxM && (N_pad + 255) / 256 >= 64);
+}
+
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 }  // namespace
@@ -510,8 +534,10 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
     if (p.S > 1) ws += align256((size_t)p.S * M * L.N_pad * 4);
     return ws;
   }
-  if (M >= env_int("OC_GEMM_MIN_M", 128))
-    return ws + align256(plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0)).part_bytes);
+  if (use_gemm(M, L.N_pad, oc::eff_group(group_size, K))) {
+    const int mt = gemm_mt(M, L.N_pad, oc::eff_group(group_size, K));
+    return ws + align256(plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0), mt).part_bytes);
+  }
   const int Mc = M < kSkinnyMaxM ? M : kSkinnyMaxM;
   const SkinnyPlan p = plan_skinny(L, Mc);
   if (p.S > 1) ws += align256((size_t)p.S * Mc * L.N_pad * 4);
@@ -569,7 +595,7 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     if (rc || p.S == 1) return rc;
     return launch_reduce(bf16, a.partial, p.S, M, N, L.N_pad, bias, y, st);
   }
-  if (M >= env_int("OC_GEMM_MIN_M", 128)) {
+  if (use_gemm(M, L.N_pad, gs)) {
     GemmArgs g;
     g.x = xa;
     g.w = (const uint8_t*)packed;
@@ -587,7 +613,8 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     g.gshift = log2_exact(gs);
     g.NKB = L.K_pad / 128;
     const bool cs4 = (gs % 128) == 0;
-    const GemmPlan gp = plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0));
+    const int mt = gemm_mt(M, L.N_pad, gs);
+    const GemmPlan gp = plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0), mt);
     g.post = nullptr;
     g.ldx = K;
     g.ldy = N;
@@ -601,26 +628,37 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     g.kper = gp.kper;
     g.part = (float*)ws;
     const dim3 grid(gp.tiles_main + gp.split_tiles * gp.S);
-    const size_t lds = 2 * kGemmXBuf;
+    const size_t lds = 2 * (size_t)(64 * mt) * 256;
     switch (bits) {
-#define OC_GM(B_)                                                                                 \
-  case B_:                                                                                        \
-    if (bf16) {                                                                                   \
-      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, true>), grid, dim3(256), lds, st, g);            \
-      else hipLaunchKernelGGL((k_gemm<B_, 1, true>), grid, dim3(256), lds, st, g);                \
-    } else {                                                                                      \
-      if (cs4) hipLaunchKernelGGL((k_gemm<B_, 4, false>), grid, dim3(256), lds, st, g);           \
-      else hipLaunchKernelGGL((k_gemm<B_, 1, false>), grid, dim3(256), lds, st, g);               \
-    }                                                                                             \
+#define OC_GM(B_)                                                                                   \
+  case B_:                                                                                          \
+    if (!cs4) {                                                                                     \
+      if (bf16) hipLaunchKernelGGL((k_gemm<B_, 1, true, 4>), grid, dim3(256), lds, st, g);          \
+      else hipLaunchKernelGGL((k_gemm<B_, 1, false, 4>), grid, dim3(256), lds, st, g);              \
+    } else if (mt == 1) {                                                                           \
+      if (bf16) hipLaunchKernelGGL((k_gemm<B_, 4, true, 1>), grid, dim3(256), lds, st, g);          \
+      else hipLaunchKernelGGL((k_gemm<B_, 4, false, 1>), grid, dim3(256), lds, st, g);              \
+    } else if (mt == 2) {                                                                           \
+      if (bf16) hipLaunchKernelGGL((k_gemm<B_, 4, true, 2>), grid, dim3(256), lds, st, g);          \
+      else hipLaunchKernelGGL((k_gemm<B_, 4, false, 2>), grid, dim3(256), lds, st, g);              \
+    } else {                                                                                        \
+      if (bf16) hipLaunchKernelGGL((k_gemm<B_, 4, true, 4>), grid, dim3(256), lds, st, g);          \
+      else hipLaunchKernelGGL((k_gemm<B_, 4, false, 4>), grid, dim3(256), lds, st, g);              \
+    }                                                                                               \
     break;
       OC_GM(2) OC_GM(3) OC_GM(4) OC_GM(8)
 #undef OC_GM
     }
     OC_HIP(hipGetLastError());
     if (gp.split_tiles > 0) {
-      const dim3 fgrid(kGemmBM * kGemmBN / 256, gp.split_tiles);
-      if (bf16) hipLaunchKernelGGL(k_gemm_fixup<true>, fgrid, dim3(256), 0, st, g);
-      else hipLaunchKernelGGL(k_gemm_fixup<false>, fgrid, dim3(256), 0, st, g);
+      const dim3 fgrid(64 * mt * kGemmBN / 256, gp.split_tiles);
+#define OC_FX(MT_)                                                                      \
+  if (mt == MT_) {                                                                      \
+    if (bf16) hipLaunchKernelGGL((k_gemm_fixup<true, MT_>), fgrid, dim3(256), 0, st, g); \
+    else hipLaunchKernelGGL((k_gemm_fixup<false, MT_>), fgrid, dim3(256), 0, st, g);     \
+  }
+      OC_FX(1) OC_FX(2) OC_FX(4)
+#undef OC_FX
       OC_HIP(hipGetLastError());
     }
     return 0;

@@ -166,6 +166,38 @@ def test_gemv_plan_variants(dev, monkeypatch, bits, w, nt):
 
 
 @pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [17, 32, 48, 64, 65, 100, 128, 130, 200])
+def test_gemm_mid_m(dev, bits, m, monkeypatch):
+    """16 < M < 256 on the tiled GEMM (tile height 64, 128 or 256 by M), with bias on even M."""
+    monkeypatch.setenv("OC_GEMM_MIN_M", "17")
+    _gemm_check(dev, _case(2048, 320 if bits == 3 else 256, bits, seed=70 + bits + m), m, "fp16", bias=m % 2 == 0)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("mt", ["1", "2", "4"])
+def test_gemm_tile_heights(dev, monkeypatch, bits, mt):
+    """Every tile height at M below, at and above it; K = 4096 on 256 columns splits the few
+    tiles along K (fp32 partials, fixup kernel)."""
+    monkeypatch.setenv("OC_GEMM_MIN_M", "17")
+    monkeypatch.setenv("OC_GEMM_MT", mt)
+    c = _case(4096, 320 if bits == 3 else 256, bits, seed=80 + bits)
+    for m in (24, 96, 160):
+        _gemm_check(dev, c, m, "fp16" if m != 96 else "bf16", bias=m == 96)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs,act,dtype,k", [(64, False, "fp16", 1024), (32, False, "bf16", 1056),
+                                            (128, True, "bf16", 2048), (-1, False, "fp16", 1056)])
+def test_gemm_mid_groups(dev, monkeypatch, bits, gs, act, dtype, k):
+    """Tiled GEMM at mid M with groups of 32/64 (256-row tiles), act-order, one group and K not
+    a multiple of the k-unit."""
+    monkeypatch.setenv("OC_GEMM_MIN_M", "17")
+    c = _case(k, 320 if bits == 3 else 272, bits, gs, act, seed=90 + bits)
+    for m in (40, 128):
+        _gemm_check(dev, c, m, dtype, bias=m == 40)
+
+
+@pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("m,k,n,gs,act,dtype", [
     (128, 1024, 256, 128, False, "fp16"),
     (300, 1056, 272, 32, False, "bf16"),     # ragged M, K not a multiple of the k-unit, N not of 256
