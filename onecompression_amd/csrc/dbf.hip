@@ -87,9 +87,10 @@ __global__ void k_sign_unpack(const uint8_t* __restrict__ bp, size_t numel, int8
 }
 
 // ---------------------------------------------------------------------------
-// sign GEMV (M <= 16 rows per launch chunk)
+// sign GEMV (M <= 16)
 // ---------------------------------------------------------------------------
 constexpr int kMaxTerms = 4;
+constexpr int kSignGemvMaxM = 16;
 
 struct TermArgs {
   const uint32_t* sg;
@@ -101,11 +102,10 @@ struct TermArgs {
 
 struct SignArgs {
   TermArgs t[kMaxTerms];
-  int unit_start[kMaxTerms + 1];  // prefix sums of NU over terms
   int n_terms;
   uint16_t* out;
   const uint16_t* bias;
-  int ld_out, M, R, RT, fill_to;
+  int ld_out, M, R, RT, fill_to, W;
 };
 
 template <bool BF16>
@@ -119,144 +119,165 @@ __device__ __forceinline__ uint32_t mul2(uint32_t a, uint32_t b) {
   }
 }
 
-// One workgroup per 16-row output tile; W waves take the (term, unit) list
-// round-robin, each keeping D units of sign words and pre-scaled x rows in
-// flight.  All terms of a launch share the same UK.
-template <int UK, int XCH, int D, int W, bool BF16>
-__global__ __launch_bounds__(64 * W) void k_sign_gemv(const SignArgs a) {
-  constexpr int XW = UK * 128 + 8;      // halfs per staged x row
-  // XCH: 16-byte x chunks per lane per unit (M * UK / 4 rounded up)
+// One workgroup per 16-row output tile; its W waves split each term's units
+// (u = wave, wave + W, ...) and keep D units in flight: the sign words, the
+// M x 128 UK slice of the input rows (XCH 16-byte chunks per lane) and, with
+// PRE, the lane's pre-scale chunk.  Every load is unconditional (invalid
+// chunks read a valid address and are zeroed after arrival), so the loads of
+// the next D - 1 units stay in flight while one unit is consumed.  The input
+// slice is multiplied by the pre scale (RNE to the activation dtype, as the
+// reference's `x * scaling0.to(x.dtype)`), bounced through a wave-private LDS
+// slot to form the A operand, and multiplied by the +-1 pairs decoded from
+// the sign words.  Terms are processed one after another (the pipeline
+// drains between them); each term's fp32 sums are multiplied by its per-row
+// post scale, then the W waves are reduced in LDS.
+//
+// Input contract: in[m, k] for Kd <= k < round8(Kd) is finite, and zero
+// unless the term has a (zero-padded) pre scale.
+template <int UK, int XCH, bool PRE, bool MULTI, bool BF16>
+__global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
+  constexpr int XW = UK * 128 + 8;  // halfs per staged x row
+  constexpr int CPR = 16 * UK;      // 16-byte chunks per row and unit
+  constexpr int VPU = UK + 4 * XCH + (PRE ? 4 : 0);
+  constexpr int D = VPU <= 8 ? 8 : (VPU <= 16 ? 4 : (VPU <= 32 ? 2 : 1));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = a.W;
   const int rt = blockIdx.x;
   const int col = lane & 15, kq = lane >> 4;
   const int n = rt * 16 + col;
   const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
   const uint32_t smask = oc_opaque(0x80008000u);
+  const int M = a.M;
 
   extern __shared__ __align__(16) uint8_t smem[];
   if (rt * 16 >= a.R) {  // padding tiles: zero-fill up to fill_to
-    for (int e = threadIdx.x; e < a.M * 16; e += 64 * W) {
+    for (int e = threadIdx.x; e < M * 16; e += 64 * W) {
       const int m = e >> 4, c = rt * 16 + (e & 15);
       if (c < a.fill_to) a.out[(size_t)m * a.ld_out + c] = 0;
     }
     return;
   }
-  const int total = a.unit_start[a.n_terms];
-  const int n_my = wave < total ? (total - wave + W - 1) / W : 0;
+  uint16_t* xslot = (uint16_t*)smem + (size_t)wave * M * XW;
+  const uint16_t* arow = xslot + min(col, M - 1) * XW + 8 * kq;
+  // chunk q of this lane: row xm[q], k offset (inside the unit) xk (the same
+  // for every q because 64 is a multiple of CPR)
+  const int xk = 8 * (lane % CPR);
+  int xm[XCH];
+#pragma unroll
+  for (int q = 0; q < XCH; ++q) xm[q] = (lane + 64 * q) / CPR;
 
-  // unit i of this wave -> (term, unit index inside the term)
-  auto locate = [&](int i, int& term, int& u) {
-    const int g = wave + W * i;
-    term = 0;
+  // Post scales of every term and the bias of this thread's output column are
+  // loaded up front (buffer loads: an absent vector reads zero at an offset
+  // past the descriptor) and converted where they are used, so that their
+  // latency hides behind the sign loads.
+  uint16_t praw[kMaxTerms];
 #pragma unroll
-    for (int q = 1; q < kMaxTerms; ++q)
-      if (q < a.n_terms && g >= a.unit_start[q]) term = q;
-    u = g - a.unit_start[term];
-  };
-
-  uint32_t sbuf[D][UK];
-  oc_u4 xbuf[D][XCH], pbuf[D][XCH];
-  int tbuf[D], ubuf[D];
-  const uint32_t one1 = BF16 ? 0x3F803F80u : 0x3C003C00u;
-  auto load_unit = [&](int i, uint32_t (&sb)[UK], oc_u4 (&xb)[XCH], oc_u4 (&pb)[XCH], int& tt, int& uu) {
-    locate(i, tt, uu);
-    const TermArgs& T = a.t[tt];
-    const uint32_t* p = T.sg + (((size_t)rt * T.NU + uu) * 64 + lane) * UK;
-    if constexpr (UK == 4) {
-      const oc_u4 v = __builtin_nontemporal_load((const oc_u4*)p);
-      sb[0] = v[0]; sb[1] = v[1]; sb[2] = v[2]; sb[3] = v[3];
-    } else {
-#pragma unroll
-      for (int q = 0; q < UK; ++q) sb[q] = __builtin_nontemporal_load(p + q);
-    }
-    // x rows of this unit and their pre scales (applied when staged):
-    // chunk c -> row c / (16 UK), k 8 * (c % (16 UK))
-#pragma unroll
-    for (int q = 0; q < XCH; ++q) {
-      const int c = lane + 64 * q;
-      const int m = c / (16 * UK), k = uu * UK * 128 + 8 * (c % (16 * UK));
-      const bool ok = m < a.M && k < T.Kd;
-      xb[q] = ok ? *(const oc_u4*)(T.in + (size_t)m * T.ld_in + k) : oc_u4{0u, 0u, 0u, 0u};
-      pb[q] = (ok && T.pre) ? *(const oc_u4*)(T.pre + k) : oc_u4{one1, one1, one1, one1};
-    }
-  };
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < n_my) load_unit(d, sbuf[d], xbuf[d], pbuf[d], tbuf[d], ubuf[d]);
-
-  uint16_t* xslot = (uint16_t*)smem + (size_t)wave * a.M * XW;
-  const uint16_t* arow = xslot + min(col, a.M - 1) * XW + 8 * kq;
-  oc_f4 accT[kMaxTerms];
-#pragma unroll
-  for (int q = 0; q < kMaxTerms; ++q) accT[q] = oc_f4{0.f, 0.f, 0.f, 0.f};
-
-  for (int i0 = 0; i0 < n_my; i0 += D) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int i = i0 + d;
-      if (i >= n_my) break;
-      oc_wave_lds_barrier();
-      const bool has_pre = a.t[tbuf[d]].pre != nullptr;
-#pragma unroll
-      for (int q = 0; q < XCH; ++q) {
-        const int c = lane + 64 * q;
-        oc_u4 v = xbuf[d][q];
-        if (has_pre) {
-#pragma unroll
-          for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], pbuf[d][q][h]);
-        }
-        if (c < a.M * 16 * UK) *(oc_u4*)(xslot + (c / (16 * UK)) * XW + 8 * (c % (16 * UK))) = v;
-      }
-      oc_wave_lds_barrier();
-      oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kbl = 0; kbl < UK; ++kbl) {
-        const uint32_t w = sbuf[d][kbl];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const oc_u4 av = *(const oc_u4*)(arow + kbl * 128 + 32 * t);
-          const int P = 4 * t;
-          const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
-                                 ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
-          acc = oc_mfma16<BF16>(av, bv, acc);
-        }
-      }
-      const int tt = tbuf[d];
-#pragma unroll
-      for (int q = 0; q < kMaxTerms; ++q)
-        if (q == tt) accT[q] += acc;
-      if (i + D < n_my) load_unit(i + D, sbuf[d], xbuf[d], pbuf[d], tbuf[d], ubuf[d]);
-    }
+  for (int q = 0; q < (MULTI ? kMaxTerms : 1); ++q) {
+    const bool ok = q < a.n_terms && a.t[q].post != nullptr && n < a.R;
+    praw[q] = __builtin_amdgcn_raw_buffer_load_b16(oc_rsrc(q < a.n_terms ? a.t[q].post : nullptr, (uint32_t)a.R * 2),
+                                                   ok ? (uint32_t)n * 2 : kOcOob, 0, 0);
   }
+  const int ecol = rt * 16 + (threadIdx.x & 15);
+  const uint16_t braw = __builtin_amdgcn_raw_buffer_load_b16(
+      oc_rsrc(a.bias, (uint32_t)a.R * 2), (a.bias && ecol < a.R) ? (uint32_t)ecol * 2 : kOcOob, 0, 0);
 
-  // post scales, then reduce the W waves
   oc_f4 y = oc_f4{0.f, 0.f, 0.f, 0.f};
+  // MULTI: several terms one after another (the pipeline drains between
+  // them); a single term is compiled without the loop (exact load waits).
+  for (int t = 0; t < (MULTI ? a.n_terms : 1); ++t) {
+    const TermArgs T = a.t[t];
+    const int n_my = wave < T.NU ? (T.NU - wave + W - 1) / W : 0;
+    uint32_t sbuf[D][UK];
+    oc_u4 xbuf[D][XCH];
+    oc_u4 pbuf[D][1];
+    // Buffer loads: input chunks at k >= Kd or rows >= M read zero (offset
+    // past the end of the descriptor, no memory access).
+    const __amdgpu_buffer_rsrc_t sr =
+        oc_rsrc(T.sg + (size_t)rt * T.NU * 64 * UK, (uint32_t)T.NU * 64 * UK * 4);
+    const __amdgpu_buffer_rsrc_t xr = oc_rsrc(T.in, (uint32_t)M * T.ld_in * 2);
+    const __amdgpu_buffer_rsrc_t pr = oc_rsrc(T.pre, (uint32_t)((T.Kd + 7) / 8 * 8) * 2);
+    auto load_unit = [&](int i, uint32_t (&sb)[UK], oc_u4 (&xb)[XCH], oc_u4 (&pb)[1]) {
+      const int u = wave + W * i;
+      const uint32_t so = (uint32_t)(u * 64 + lane) * UK * 4;
+      if constexpr (UK == 4) {
+        const oc_u4 v = oc_bload16_nt(sr, so);
+        sb[0] = v[0]; sb[1] = v[1]; sb[2] = v[2]; sb[3] = v[3];
+      } else if constexpr (UK == 2) {
+        typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+        const u2v v = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(sr, so, 0, 2));
+        sb[0] = v[0]; sb[1] = v[1];
+      } else {
+        sb[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 2);
+      }
+      const int k = u * UK * 128 + xk;
+      const bool kok = k < T.Kd;
 #pragma unroll
-  for (int q = 0; q < kMaxTerms; ++q) {
-    if (q >= a.n_terms) break;
-    float ps = 1.f;
-    if (a.t[q].post && n < a.R) ps = BF16 ? oc_bf2f(a.t[q].post[n]) : oc_h2f(a.t[q].post[n]);
-    y += ps * accT[q];
+      for (int q = 0; q < XCH; ++q)
+        xb[q] = oc_bload16(xr, kok && xm[q] < M ? (uint32_t)(xm[q] * T.ld_in + k) * 2 : kOcOob);
+      if constexpr (PRE) pb[0] = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < n_my) load_unit(d, sbuf[d], xbuf[d], pbuf[d]);
+
+    oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < n_my; i0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int i = i0 + d;
+        if (i >= n_my) break;
+        // Lanes read what other lanes of the same wave wrote: the compiler
+        // barriers order the exchange (a wave's DS operations run in order).
+        oc_wave_lds_barrier();
+#pragma unroll
+        for (int q = 0; q < XCH; ++q) {
+          oc_u4 v = xbuf[d][q];
+          if constexpr (PRE) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], pbuf[d][0][h]);
+          }
+          if (xm[q] < M) *(oc_u4*)(xslot + xm[q] * XW + xk) = v;
+        }
+        oc_wave_lds_barrier();
+#pragma unroll
+        for (int kbl = 0; kbl < UK; ++kbl) {
+          const uint32_t w = sbuf[d][kbl];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const oc_u4 av = *(const oc_u4*)(arow + kbl * 128 + 32 * s);
+            const int P = 4 * s;
+            const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
+                                   ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
+            acc = oc_mfma16<BF16>(av, bv, acc);
+          }
+        }
+        if (i + D < n_my) load_unit(i + D, sbuf[d], xbuf[d], pbuf[d]);
+      }
+    }
+    uint16_t pr16 = praw[0];
+#pragma unroll
+    for (int q = 1; q < (MULTI ? kMaxTerms : 1); ++q)
+      if (q == t) pr16 = praw[q];
+    const float ps = (T.post && n < a.R) ? (BF16 ? oc_bf2f(pr16) : oc_h2f(pr16)) : 1.f;
+    y += ps * acc;
   }
-  __syncthreads();
+
+  // reduce the W waves
+  __syncthreads();  // x slots no longer needed: reuse LDS
   float* red = (float*)smem;  // [W][4][64]
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = y[r];
   __syncthreads();
-  for (int e = threadIdx.x; e < 256; e += 64 * W) {
+  if (threadIdx.x < 256) {
+    const int e = threadIdx.x;
+    const float bval = BF16 ? oc_bf2f(braw) : oc_h2f(braw);
     float v = 0.f;
-#pragma unroll
     for (int ww = 0; ww < W; ++ww) v += red[ww * 256 + e];
     const int ln = e & 63, r = e >> 6;
     const int m = 4 * (ln >> 4) + r, c = rt * 16 + (ln & 15);
-    if (m >= a.M || c >= a.fill_to) continue;
-    if (c < a.R) {
-      if (a.bias) v += BF16 ? oc_bf2f(a.bias[c]) : oc_h2f(a.bias[c]);
-      a.out[(size_t)m * a.ld_out + c] = BF16 ? oc_f2bf(v) : oc_f2h(v);
-    } else {
-      a.out[(size_t)m * a.ld_out + c] = 0;
-    }
+    if (m < M && c < a.fill_to)
+      a.out[(size_t)m * a.ld_out + c] = c < a.R ? (BF16 ? oc_f2bf(v + bval) : oc_f2h(v + bval)) : (uint16_t)0;
   }
 }
 
@@ -265,32 +286,52 @@ int env_int(const char* name, int dflt) {
   return v && *v ? atoi(v) : dflt;
 }
 
-constexpr size_t kSignLds = 96 * 1024;
+constexpr size_t kSignLds = 64 * 1024;
+
+// Waves per workgroup (4, 8 or 16): enough waves in total to cover the GPU
+// (the rank-side stage has few row tiles), no more than the units allow, and
+// an LDS x slot per wave.
+int sign_waves(int RT, int NU, int M, int UK) {
+  const int e = env_int("OC_SIGN_W", 0);
+  int w = (e == 4 || e == 8 || e == 16) ? e : (RT >= 768 ? 4 : (RT >= 384 ? 8 : 16));
+  while (w > 4 && w > NU) w /= 2;
+  const size_t slot = (size_t)M * (UK * 128 + 8) * 2;
+  while (w > 4 && slot * w > kSignLds) w /= 2;
+  return w;
+}
 
 template <int UK, int XCH, bool BF16>
-int launch_sign_x(const SignArgs& a, int rt_grid, int w, hipStream_t st) {
-  constexpr int D = XCH >= 8 ? 1 : (XCH >= 4 ? 2 : (UK == 1 ? 8 : 4));
+int launch_sign_x(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
   const size_t slot = (size_t)a.M * (UK * 128 + 8) * 2;
-  if (XCH > UK && w > 8) w = 8;  // keeps the wider x ring within 256 VGPRs
-  while (w > 4 && slot * w > kSignLds) w /= 2;
-  const size_t xb = slot * w;
-  const size_t rb = (size_t)w * 4 * 64 * 4;
+  const size_t xb = slot * a.W;
+  const size_t rb = (size_t)a.W * 4 * 64 * 4;
   const size_t lds = ((xb > rb ? xb : rb) + 15) / 16 * 16;
-  if (w == 4)
-    hipLaunchKernelGGL((k_sign_gemv<UK, XCH, D, 4, BF16>), dim3(rt_grid), dim3(256), lds, st, a);
-  else if (XCH > UK || w == 8)
-    hipLaunchKernelGGL((k_sign_gemv<UK, XCH, D, 8, BF16>), dim3(rt_grid), dim3(512), lds, st, a);
-  else
-    hipLaunchKernelGGL((k_sign_gemv<UK, UK, D, 16, BF16>), dim3(rt_grid), dim3(1024), lds, st, a);
+  const dim3 g(rt_grid), b(64 * a.W);
+  if (a.n_terms > 1) {
+    if (pre) hipLaunchKernelGGL((k_sign_gemv<UK, XCH, true, true, BF16>), g, b, lds, st, a);
+    else hipLaunchKernelGGL((k_sign_gemv<UK, XCH, false, true, BF16>), g, b, lds, st, a);
+  } else {
+    if (pre) hipLaunchKernelGGL((k_sign_gemv<UK, XCH, true, false, BF16>), g, b, lds, st, a);
+    else hipLaunchKernelGGL((k_sign_gemv<UK, XCH, false, false, BF16>), g, b, lds, st, a);
+  }
   OC_HIP(hipGetLastError());
   return 0;
 }
 
+// XCH = 16-byte input chunks per lane and unit: M * 16 UK chunks over 64 lanes.
 template <int UK, bool BF16>
-int launch_sign(const SignArgs& a, int rt_grid, int w, hipStream_t st) {
-  const int xc = (a.M * UK + 3) / 4;  // chunks per lane
-  if (xc <= UK) return launch_sign_x<UK, UK, BF16>(a, rt_grid, w, st);
-  return launch_sign_x<UK, 4 * UK, BF16>(a, rt_grid, w, st);
+int launch_sign(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
+  const int xc = (a.M * UK + 3) / 4;
+  if (xc <= 1) return launch_sign_x<UK, 1, BF16>(a, pre, rt_grid, st);
+  if (xc <= 2) return launch_sign_x<UK, 2, BF16>(a, pre, rt_grid, st);
+  if (xc <= 4) return launch_sign_x<UK, 4, BF16>(a, pre, rt_grid, st);
+  if constexpr (UK >= 2) {
+    if (xc <= 8) return launch_sign_x<UK, 8, BF16>(a, pre, rt_grid, st);
+  }
+  if constexpr (UK == 4) {
+    if (xc <= 16) return launch_sign_x<UK, 16, BF16>(a, pre, rt_grid, st);
+  }
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no sign GEMV for M=%d UK=%d", a.M, UK);
 }
 
 }  // namespace
@@ -328,14 +369,14 @@ extern "C" int oc_dbf_prepare(const uint8_t* bp, int R, int Kd, void* packed, vo
 namespace {
 
 // ---------------------------------------------------------------------------
-// M >= kSignGemmMinM: the shared large-M GEMM core with the sign decoder.
+// M > 16: the shared GEMM core with the sign decoder, 64 MT x 256 tiles.
 // A term with a pre scale first writes RNE(in * pre) (the reference's
 // `x * scaling0.to(x.dtype)`) to the workspace; the MFMA B operand is then the
 // exact +-1 pair.  One term: one k_gemm launch (+ fixup for a split tail).
 // Several terms: one launch per term, every tile written as an fp32 partial
 // (post-scaled) into its slot, then one fixup sums the slots and adds bias.
 // ---------------------------------------------------------------------------
-int sign_gemm_min_m() { return env_int("OC_SIGN_GEMM_MIN_M", 128); }
+int sign_gemm_min_m() { return env_int("OC_SIGN_GEMM_MIN_M", kSignGemvMaxM + 1); }
 
 int round8(int v) { return (v + 7) / 8 * 8; }
 
@@ -362,14 +403,17 @@ __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int 
 
 struct SignGemmPlan {
   oc_gemm::GemmPlan gp;  // tiling of one term
+  int mt;                // tile height 64 mt
   size_t xs_off[kMaxTerms], part_off, bytes;
 };
 
 SignGemmPlan plan_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R) {
   SignGemmPlan p;
   const SignLayout L = make_sign_layout(R, terms[0].Kd);
+  const int e = env_int("OC_GEMM_MT", 0);
+  p.mt = (e == 1 || e == 2 || e == 4) ? e : oc_gemm::gemm_tile_height(M, L.RT * 16);
   // several terms are summed through partial slots: no K split inside a term
-  p.gp = oc_gemm::plan_gemm(M, L.RT * 16, L.K_pad, n_terms > 1 ? 1 : env_int("OC_GEMM_SPLIT", 0));
+  p.gp = oc_gemm::plan_gemm(M, L.RT * 16, L.K_pad, n_terms > 1 ? 1 : env_int("OC_GEMM_SPLIT", 0), p.mt);
   size_t off = 0;
   for (int i = 0; i < n_terms; ++i) {
     p.xs_off[i] = off;
@@ -377,7 +421,7 @@ SignGemmPlan plan_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
   }
   p.part_off = off;
   if (n_terms > 1)
-    off += (size_t)p.gp.MB * p.gp.NB * n_terms * oc_gemm::kGemmBM * oc_gemm::kGemmBN * 4;
+    off += (size_t)p.gp.MB * p.gp.NB * n_terms * (64 * p.mt) * oc_gemm::kGemmBN * 4;
   else
     off += align256(p.gp.part_bytes);
   p.bytes = off;
@@ -385,8 +429,19 @@ SignGemmPlan plan_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
 }
 
 template <bool BF16>
-void launch_sign_gemm_term(const oc_gemm::GemmArgs& g, int grid, hipStream_t st) {
-  hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16>), dim3(grid), dim3(256), 2 * oc_gemm::kGemmXBuf, st, g);
+void launch_sign_gemm_term(const oc_gemm::GemmArgs& g, int mt, int grid, hipStream_t st) {
+  const size_t lds = 2 * (size_t)(64 * mt) * 256;
+  if (mt == 1) hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 1>), dim3(grid), dim3(256), lds, st, g);
+  else if (mt == 2) hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 2>), dim3(grid), dim3(256), lds, st, g);
+  else hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 4>), dim3(grid), dim3(256), lds, st, g);
+}
+
+template <bool BF16>
+void launch_sign_fixup(const oc_gemm::GemmArgs& g, int mt, int tiles, hipStream_t st) {
+  const dim3 fg(64 * mt * oc_gemm::kGemmBN / 256, tiles);
+  if (mt == 1) hipLaunchKernelGGL((oc_gemm::k_gemm_fixup<BF16, 1>), fg, dim3(256), 0, st, g);
+  else if (mt == 2) hipLaunchKernelGGL((oc_gemm::k_gemm_fixup<BF16, 2>), fg, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((oc_gemm::k_gemm_fixup<BF16, 4>), fg, dim3(256), 0, st, g);
 }
 
 int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool bf16, const void* bias,
@@ -450,8 +505,8 @@ int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool b
       g.poff = i;
     }
     const int grid = n_terms == 1 ? p.gp.tiles_main + p.gp.split_tiles * p.gp.S : p.gp.MB * p.gp.NB;
-    if (bf16) launch_sign_gemm_term<true>(g, grid, st);
-    else launch_sign_gemm_term<false>(g, grid, st);
+    if (bf16) launch_sign_gemm_term<true>(g, p.mt, grid, st);
+    else launch_sign_gemm_term<false>(g, p.mt, grid, st);
     OC_HIP(hipGetLastError());
     if (i == n_terms - 1) {
       const int fix_tiles = n_terms == 1 ? p.gp.split_tiles : p.gp.MB * p.gp.NB;
@@ -459,9 +514,8 @@ int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool b
         g.bias = (const uint16_t*)bias;
         g.tiles_main = n_terms == 1 ? p.gp.tiles_main : 0;
         g.pstride = n_terms == 1 ? p.gp.S : n_terms;
-        const dim3 fg(oc_gemm::kGemmBM * oc_gemm::kGemmBN / 256, fix_tiles);
-        if (bf16) hipLaunchKernelGGL(oc_gemm::k_gemm_fixup<true>, fg, dim3(256), 0, st, g);
-        else hipLaunchKernelGGL(oc_gemm::k_gemm_fixup<false>, fg, dim3(256), 0, st, g);
+        if (bf16) launch_sign_fixup<true>(g, p.mt, fix_tiles, st);
+        else launch_sign_fixup<false>(g, p.mt, fix_tiles, st);
         OC_HIP(hipGetLastError());
       }
     }
@@ -495,7 +549,8 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
   OC_REQUIRE(ld_out >= fill_to, OC_ERR_SHAPE, "ld_out=%d < fill_to=%d", ld_out, fill_to);
   if (M == 0) return 0;
   SignArgs a;
-  int uk = 0, start = 0;
+  int uk = 0;
+  bool pre = terms[0].pre != nullptr;
   for (int i = 0; i < n_terms; ++i) {
     const oc_sign_term& T = terms[i];
     OC_REQUIRE(T.packed && T.in, OC_ERR_INVALID, "term %d: null pointer", i);
@@ -503,6 +558,8 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
                "term %d: Kd=%d / ld_in=%d (ld_in must be >= Kd and a multiple of 8)", i, T.Kd, T.ld_in);
     const SignLayout L = make_sign_layout(R, T.Kd);
     OC_REQUIRE(uk == 0 || uk == L.UK, OC_ERR_UNSUPPORTED, "terms of one call need the same unit size");
+    OC_REQUIRE((T.pre != nullptr) == pre, OC_ERR_UNSUPPORTED,
+               "terms of one call must all have a pre scale or none");
     uk = L.UK;
     a.t[i].sg = (const uint32_t*)T.packed;
     a.t[i].in = (const uint16_t*)T.in;
@@ -512,10 +569,7 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
     a.t[i].Kd = T.Kd;
     a.t[i].NU = L.NU;
     a.t[i].UK = L.UK;
-    a.unit_start[i] = start;
-    start += L.NU;
   }
-  for (int i = n_terms; i <= kMaxTerms; ++i) a.unit_start[i] = start;
   if (M >= sign_gemm_min_m())
     return sign_gemm_large(terms, n_terms, M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to,
                            workspace, ws_bytes, (hipStream_t)stream);
@@ -525,23 +579,26 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
   a.RT = (R + 15) / 16;
   a.fill_to = fill_to;
   a.ld_out = ld_out;
+  int nu_min = a.t[0].NU;
+  for (int i = 1; i < n_terms; ++i) nu_min = a.t[i].NU < nu_min ? a.t[i].NU : nu_min;
   const int rt_grid = (fill_to + 15) / 16;
-  int w = env_int("OC_SIGN_W", 0);
-  if (w != 4 && w != 8 && w != 16) w = a.RT >= 512 ? 8 : 16;
   hipStream_t st = (hipStream_t)stream;
   const bool bf16 = act_dtype == OC_DTYPE_BF16;
-  for (int m0 = 0; m0 < M; m0 += 16) {
+  // Rows in chunks of 16 (only reached below the GEMM threshold, i.e. when
+  // OC_SIGN_GEMM_MIN_M raises it).
+  for (int m0 = 0; m0 < M; m0 += kSignGemvMaxM) {
     SignArgs c = a;
-    c.M = M - m0 < 16 ? M - m0 : 16;
+    c.M = M - m0 < kSignGemvMaxM ? M - m0 : kSignGemvMaxM;
+    c.W = sign_waves(a.RT, nu_min, c.M, uk);
     c.out = (uint16_t*)out + (size_t)m0 * ld_out;
     for (int i = 0; i < n_terms; ++i) c.t[i].in = a.t[i].in + (size_t)m0 * a.t[i].ld_in;
     int rc;
     if (uk == 4)
-      rc = bf16 ? launch_sign<4, true>(c, rt_grid, w, st) : launch_sign<4, false>(c, rt_grid, w, st);
+      rc = bf16 ? launch_sign<4, true>(c, pre, rt_grid, st) : launch_sign<4, false>(c, pre, rt_grid, st);
     else if (uk == 2)
-      rc = bf16 ? launch_sign<2, true>(c, rt_grid, w, st) : launch_sign<2, false>(c, rt_grid, w, st);
+      rc = bf16 ? launch_sign<2, true>(c, pre, rt_grid, st) : launch_sign<2, false>(c, pre, rt_grid, st);
     else
-      rc = bf16 ? launch_sign<1, true>(c, rt_grid, w, st) : launch_sign<1, false>(c, rt_grid, w, st);
+      rc = bf16 ? launch_sign<1, true>(c, pre, rt_grid, st) : launch_sign<1, false>(c, pre, rt_grid, st);
     if (rc) return rc;
   }
   return 0;

@@ -455,6 +455,16 @@ struct GemmPlan {
 
 inline int device_cus() { return oc_device_cus(); }
 
+// Tile height (64 MT rows, 256 columns) for M rows: the tallest that still
+// leaves at least half as many tiles as CUs (measured: fewer, taller tiles
+// lose to more, shorter ones until the grid covers the GPU).
+inline int gemm_tile_height(int M, int N_pad) {
+  const int NB = (N_pad + kGemmBN - 1) / kGemmBN, C = device_cus();
+  for (int mt = 4; mt > 1; mt /= 2)
+    if (((M + 64 * mt - 1) / (64 * mt)) * NB * 2 >= C) return mt;
+  return 1;
+}
+
 // M rows, N_pad columns (multiple of 16), K_pad = 128 * k-blocks; split_env
 // forces the piece count (1 = never split, 0 = automatic).
 inline GemmPlan plan_gemm(int M, int N_pad, int K_pad, int split_env, int MT = 4) {

@@ -495,18 +495,13 @@ int launch_reduce(bool bf16, const float* partial, int S, int M, int N, int N_pa
 
 constexpr int kSkinnyMaxM = 64;
 
-// Tile height of the GEMM for M rows (64 MT rows, 256 columns): the tallest
-// that still leaves at least half as many tiles as CUs (measured: fewer,
-// taller tiles lose to more, shorter ones until the grid covers the GPU);
-// only 256-row tiles for groups that are not multiples of 128.
+// Tile height of the GEMM for M rows (64 MT rows, 256 columns): see
+// gemm_tile_height; only 256-row tiles for groups that are not multiples of 128.
 int gemm_mt(int M, int N_pad, int gs) {
   const int e = env_int("OC_GEMM_MT", 0);
   if ((gs % 128) != 0) return 4;
   if (e == 1 || e == 2 || e == 4) return e;
-  const int NB = (N_pad + 255) / 256, C = device_cus();
-  for (int mt = 4; mt > 1; mt /= 2)
-    if (((M + 64 * mt - 1) / (64 * mt)) * NB * 2 >= C) return mt;
-  return 1;
+  return gemm_tile_height(M, N_pad);
 }
 
 // The tiled GEMM from M = 33 (17 when there are 64 or more column tiles; 128

@@ -102,6 +102,21 @@ __device__ __forceinline__ uint32_t oc_opaque(uint32_t v) {
 // address.  Emits no instruction.
 __device__ __forceinline__ void oc_wave_lds_barrier() { asm volatile("" ::: "memory"); }
 
+// Raw buffer resource over [base, base + bytes).  A load at an offset past
+// `bytes` returns zero without touching memory; kOcOob is such an offset for
+// every buffer this library reads (all are below 2 GiB per descriptor).
+constexpr uint32_t kOcOob = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t oc_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, bytes, 0x00020000);
+}
+// 16-byte buffer loads: plain, and streaming (nt: read once, not kept in L2)
+__device__ __forceinline__ oc_u4 oc_bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(oc_u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ oc_u4 oc_bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(oc_u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+
 // Compute units of the current device (cached per device; 256 if unknown).
 inline int oc_device_cus() {
   static int cus[64] = {0};

@@ -135,8 +135,8 @@ def _mdbf_path(n, m, r, l, seed):
                 A_amp=amp(n, l), B_amp=amp(m, l), Q_U_amp=amp(r, l), Q_V_amp=amp(r, l))
 
 
-@pytest.mark.parametrize("P,l,m_rows", [(2, 1, 1), (2, 1, 32), (1, 2, 4), (2, 2, 1),
-                                        (2, 1, 200), (1, 2, 150), (2, 2, 140)])  # large-M: partial slots
+@pytest.mark.parametrize("P,l,m_rows", [(2, 1, 1), (2, 1, 32), (1, 2, 4), (2, 2, 1), (2, 2, 16),
+                                        (2, 1, 200), (1, 2, 150), (2, 2, 140)])  # M > 16: partial slots
 def test_mdbf_forward(dev, P, l, m_rows):
     n, m = 384, 256
     r = od.mid_features(1.0, m, n)
@@ -150,10 +150,11 @@ def test_mdbf_forward(dev, P, l, m_rows):
     assert _rel(y, ref) <= 1e-2, _rel(y, ref)
 
 
+@pytest.mark.parametrize("m", [1, 5, 16, 40, 140])  # GEMV (M <= 16) and the GEMM core (tile heights 64..256)
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-def test_sign_gemm_large_fill_and_bias(dev, dtype):
-    """Large-M sign matmul: pre/post scales, bias, zero columns R..fill_to, ld_out > fill_to."""
-    m, kd, R, fill_to, ld_out = 140, 300, 37, 40, 48
+def test_sign_gemm_fill_and_bias(dev, dtype, m):
+    """Sign matmul: pre/post scales, bias, zero columns R..fill_to, ld_out > fill_to."""
+    kd, R, fill_to, ld_out = 300, 37, 40, 48
     rng = np.random.default_rng(7)
     signs = rng.choice([-1, 1], size=(R, kd))
     f = dbf_ops.sign_prepare(_t(od.pack_binary(signs), dev), R, kd)
