@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 2
+#define OC_ABI_VERSION 3
 
 enum {
   OC_OK = 0,
@@ -110,6 +110,33 @@ size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int group_size, in
 int oc_gptq_gemm(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
                  const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
                  void* y, void* workspace, size_t ws_bytes, void* stream);
+
+/* One part of a fused GPTQ module (e.g. q, k and v of qkv_proj): its repacked weights
+ * (oc_gptq_prepare), act-order permutation or NULL, bias [N] or NULL, width, bits, group size. */
+typedef struct {
+  const void* packed;
+  const uint32_t* meta;
+  const int32_t* perm;
+  const void* bias;
+  int N;
+  int bits;
+  int group_size;
+} oc_gptq_part;
+
+/* Workspace bytes oc_gptq_gemm_grouped needs for these parts at M rows (host only). */
+size_t oc_gptq_grouped_workspace_bytes(const oc_gptq_part* parts, int n_parts, int M, int K);
+
+/* y[:, off_p : off_p + N_p] = x[M, K] @ dequant(W_p)^T (+ bias_p) for every part p, where off_p is
+ * the sum of the widths of the parts before p; y has row stride ldy >= sum N_p.  The parts may
+ * differ in bits, group size and act-order: at M <= 16 with groups that are multiples of 128 they
+ * run as one launch, otherwise one after the other (same results either way).  Workspace,
+ * threading and capture rules as oc_gptq_gemm.
+ * The reference rejects fused modules whose shards differ in their quantization settings
+ * (vllm_plugins/gptq/vllm_plugin.py:310-317 via utils/module.py:153-177); this entry point serves
+ * them, e.g. Mixed-GPTQ qkv_proj with q at 4 bits and k, v at 8 bits as one apply(). */
+int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_part* parts, int n_parts,
+                         int act_dtype, void* y, int ldy, void* workspace, size_t ws_bytes,
+                         void* stream);
 
 /* ---------------------------------------------------------------- DBF / MDBF ---------------- */
 

@@ -33,6 +33,8 @@ SIGNATURES = {
     "oc_gptq_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "oc_gptq_gemm": (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P, P,
                              c_size_t, P]),
+    "oc_gptq_grouped_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
+    "oc_gptq_gemm_grouped": (c_int, [P, c_int, c_int, P, c_int, c_int, P, c_int, P, c_size_t, P]),
     "oc_dbf_layout": (c_int, [c_int, c_int, c_size_t_p, c_int_p, c_int_p]),
     "oc_dbf_unpack_signs": (c_int, [P, c_int, c_int, P, P]),
     "oc_dbf_prepare": (c_int, [P, c_int, c_int, P, P]),
@@ -43,7 +45,7 @@ SIGNATURES = {
     "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, c_size_t, P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
 OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2
 ERR_NAMES = {-1: "INVALID", -2: "UNSUPPORTED", -3: "SHAPE", -4: "HIP", -5: "WORKSPACE", -6: "GIDX"}

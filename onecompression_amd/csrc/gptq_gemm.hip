@@ -34,6 +34,7 @@ struct SkinnyArgs {
   uint16_t* y;
   float* partial;      // [S, M, N_pad] fp32 when S > 1
   int M, K, N, N_pad, NT_total, NU, G, gs, S, ups;
+  int ldy;  // row stride of y
 };
 
 template <int BITS, int MB, int NT, bool BF16>
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void k_skinny(const SkinnyArgs a) {
       if (n < a.N) {
         float o = v;
         if (a.bias) o += BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
-        a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
+        a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
       }
     } else {
       part[(size_t)m * a.N_pad + n] = v;
@@ -166,10 +167,13 @@ struct GemvArgs {
   uint16_t* y;
   float* partial;
   int M, K, N, N_pad, NT_total, NU, G, gs, gshift, S, ups;
+  int ldy;   // row stride of y (N, or the fused width for a part of a fused layer)
+  int bits;  // the part's bit width (grouped launches pick the decoder by it)
 };
 
+// One workgroup's share of a GEMV launch: block = column group * S + split.
 template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16>
-__global__ __launch_bounds__(64 * W) void k_gemv(const GemvArgs a) {
+__device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
   using GG = Geo<BITS>;
   constexpr int U = GG::U, P = GG::P;
   constexpr int SPK = 4 / CS;        // correction segments per k-block
@@ -178,7 +182,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(const GemvArgs a) {
   constexpr float OFF = dec_offset<BITS, BF16>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ntg = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  const int ntg = block / a.S, s = block % a.S;
   const int col = lane & 15, kq = lane >> 4;
   const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<BF16>());
   const uint32_t one16 = BF16 ? 0x3F803F80u : 0x3C003C00u;
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(const GemvArgs a) {
       if (n < a.N) {
         float o = v;
         if (a.bias) o += BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
-        a.y[(size_t)m * a.N + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
+        a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
       }
     } else {
       part[(size_t)m * a.N_pad + n] = v;
@@ -314,17 +318,219 @@ __global__ __launch_bounds__(64 * W) void k_gemv(const GemvArgs a) {
   }
 }
 
+template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16>
+__global__ __launch_bounds__(64 * W) void k_gemv(const GemvArgs a) {
+  gemv_tile<BITS, NT, CS, D, W, XCH, BF16>(a, blockIdx.x);
+}
+
+// Units in flight per wave for BITS and NT n-tiles per workgroup.
+template <int BITS, int NT, int XCH>
+struct GemvDepth {
+  static constexpr int DB = (BITS == 3 || BITS == 8) ? 2 : 4;
+  static constexpr int D = XCH >= 8 ? 1 : (DB / NT > 0 ? DB / NT : 1);
+};
+
+// Several layers that read the same activations (the parts of a fused
+// module, which may differ in bit width) in one launch: workgroup b belongs
+// to part p for block_start[p] <= b < block_start[p + 1] and runs that part's
+// decoder (a uniform branch on its bit width).
+constexpr int kMaxParts = 4;
+struct GemvGroupArgs {
+  GemvArgs part[kMaxParts];
+  int block_start[kMaxParts + 1];
+  int n_parts;
+};
+
+template <int NT, int W, int XCH, bool BF16>
+__global__ __launch_bounds__(64 * W) void k_gemv_group(const GemvGroupArgs g) {
+  int p = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxParts; ++q)
+    if (q < g.n_parts && (int)blockIdx.x >= g.block_start[q]) p = q;
+  const GemvArgs& a = g.part[p];
+  const int b = blockIdx.x - g.block_start[p];
+  switch (a.bits) {
+    case 2: gemv_tile<2, NT, 4, GemvDepth<2, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+    case 3: gemv_tile<3, NT, 4, GemvDepth<3, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+    case 4: gemv_tile<4, NT, 4, GemvDepth<4, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+    default: gemv_tile<8, NT, 4, GemvDepth<8, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wide layers at small M (thousands of n-tiles, e.g. a fused gate|up): one
+// wave per n-tile streams the whole K of its 16 columns through a ring of D
+// units, so memory and the decode overlap for the wave's whole life and no
+// cross-wave reduction is needed.  The workgroup (4 waves, 4 consecutive
+// n-tiles) stages all M x K of x in LDS once, together with the sums of x over
+// each k-block that the zero-point correction needs (so no MFMA is spent on
+// them).  Every wave runs the same number of units (NU, a multiple of D), so
+// the loads are unconditional and the compiler's vmcnt waits are exact:
+// prologue (D units), steady state (consume a slot, refill it D units ahead),
+// drain (the last D units).  Groups are a power of two >= 128 (one
+// scale/zero word per k-block).  MR = the output rows 4 kq + r (r < MR) a
+// lane accumulates (MR = 1 for M = 1).
+// ---------------------------------------------------------------------------
+struct StreamArgs {
+  const uint16_t* x;
+  const uint8_t* w;
+  const uint32_t* meta;
+  const uint16_t* bias;
+  uint16_t* y;
+  int M, K, K_pad, N, N_pad, NT_total, NU, G, gs, gkb_shift, ldy;
+};
+
+template <int BITS, int D, int MR, int KS, bool BF16>
+__global__ __launch_bounds__(256, 4) void k_gemv_stream(const StreamArgs a) {
+  using GG = Geo<BITS>;
+  constexpr int U = GG::U, P = GG::P;
+  constexpr float OFF = dec_offset<BITS, BF16>();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, kq = lane >> 4;
+  const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<BF16>());
+  // KS waves share an n-tile, each taking NU / KS consecutive units
+  const int nt = blockIdx.x * (4 / KS) + wave / KS, ks = wave % KS;
+  const int nu = a.NU / KS, ub = ks * nu;
+  const int M = a.M;
+
+  // LDS: x rows [M][K_pad + 8] (zero past K), then group sums [G][16] fp32
+  extern __shared__ __align__(16) uint16_t xl[];
+  const int XL = a.K_pad + 8;  // halfs per LDS row
+  float* xsum = (float*)(xl + (size_t)M * XL);
+  const int cpr = a.K_pad / 8;
+  for (int c = threadIdx.x; c < M * cpr; c += 256) {
+    const int m = c / cpr, k = 8 * (c % cpr);
+    oc_u4 v = oc_u4{0u, 0u, 0u, 0u};
+    if (k < a.K) v = *(const oc_u4*)(a.x + (size_t)m * a.K + k);
+    *(oc_u4*)(xl + m * XL + k) = v;
+  }
+  const bool has_bias = a.bias != nullptr;
+  const uint16_t braw = __builtin_amdgcn_raw_buffer_load_b16(
+      oc_rsrc(a.bias, (uint32_t)a.N * 2), has_bias && nt * 16 + col < a.N ? (uint32_t)(nt * 16 + col) * 2 : kOcOob,
+      0, 0);
+  __syncthreads();
+  // sum of x over each k-block of 128 for rows < M (fp32): 16 lanes per sum,
+  // 8 values each, then a 16-lane butterfly.  Entries of rows >= M stay
+  // unset: they only reach accumulators of rows that are never stored.
+  const int nkb = a.K_pad / 128;
+  for (int c = threadIdx.x; c < M * nkb * 16; c += 256) {
+    const int e = c >> 4, kb = e % nkb, m = e / nkb;
+    const oc_u4 v = *(const oc_u4*)(xl + m * XL + kb * 128 + 8 * (c & 15));
+    float sum = 0.f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const uint32_t pr = v[h];
+      sum += (BF16 ? oc_bf2f((uint16_t)(pr & 0xFFFFu)) : oc_h2f((uint16_t)(pr & 0xFFFFu))) +
+             (BF16 ? oc_bf2f((uint16_t)(pr >> 16)) : oc_h2f((uint16_t)(pr >> 16)));
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+    if ((c & 15) == 0) xsum[kb * 16 + m] = sum;
+  }
+  __syncthreads();
+  if (KS == 1 && nt >= a.NT_total) return;  // a whole wave past the last n-tile (no barrier follows)
+
+  const int ntc = min(nt, a.NT_total - 1);  // KS > 1: waves past the last n-tile recompute it, unused
+  const __amdgpu_buffer_rsrc_t wr = oc_rsrc(a.w + (size_t)ntc * a.NU * P * 1024, (uint32_t)a.NU * P * 1024);
+  const __amdgpu_buffer_rsrc_t mr = oc_rsrc(a.meta, (uint32_t)a.G * a.N_pad * 4);
+  const uint16_t* arow = xl + min(col, M - 1) * XL + 8 * kq;
+  const float* srow = xsum + 4 * kq;
+  const uint32_t mcol = (uint32_t)(ntc * 16 + col) * 4;
+  uint32_t wb[D][4 * P];
+  uint32_t mb[D][U];
+  auto load = [&](int u, uint32_t (&w)[4 * P], uint32_t (&m)[U]) {
+#pragma unroll
+    for (int pt = 0; pt < P; ++pt) {
+      const oc_u4 v = oc_bload16_nt(wr, (uint32_t)(u * P + pt) * 1024 + lane * 16);
+      w[4 * pt] = v[0];
+      w[4 * pt + 1] = v[1];
+      w[4 * pt + 2] = v[2];
+      w[4 * pt + 3] = v[3];
+    }
+#pragma unroll
+    for (int kbl = 0; kbl < U; ++kbl) {
+      const int g = (u * U + kbl) >> a.gkb_shift;
+      m[kbl] = __builtin_amdgcn_raw_buffer_load_b32(mr, mcol + (uint32_t)(g * a.N_pad) * 4, 0, 0);
+    }
+  };
+  oc_f4 yacc = oc_f4{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int u, const uint32_t (&w)[4 * P], const uint32_t (&m)[U]) {
+#pragma unroll
+    for (int kbl = 0; kbl < U; ++kbl) {
+      const int kb = u * U + kbl;
+      oc_u4 av[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[t] = *(const oc_u4*)(arow + kb * 128 + 32 * t);
+      oc_u4 bq[4];
+      decode_kblock<BITS, BF16>(w, kbl, bq, msk, mag);
+      oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(av[t], bq[t], acc);
+      const uint32_t md = m[kbl];
+      const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
+      const float oz = OFF + (float)(md >> 16);
+      const float* sg = srow + kb * 16;
+      if constexpr (MR == 1) {
+        yacc[0] = fmaf(sc, fmaf(-oz, sg[0], acc[0]), yacc[0]);
+      } else {
+        const oc_f4 xs = *(const oc_f4*)sg;
+#pragma unroll
+        for (int r = 0; r < MR; ++r) yacc[r] = fmaf(sc, fmaf(-oz, xs[r], acc[r]), yacc[r]);
+      }
+    }
+  };
+  // prologue, steady state, drain (NU / KS is a multiple of D and at least D)
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load(ub + d, wb[d], mb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i0 = 0; i0 < nu - D; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(ub + i0 + d, wb[d], mb[d]);
+      load(ub + i0 + D + d, wb[d], mb[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) consume(ub + nu - D + d, wb[d], mb[d]);
+  if constexpr (KS > 1) {
+    // the KS partial sums of an n-tile meet in LDS (reusing the x rows)
+    __syncthreads();
+    float* red = (float*)xl;  // [4 waves][MR][64]
+#pragma unroll
+    for (int r = 0; r < MR; ++r) red[(wave * MR + r) * 64 + lane] = yacc[r];
+    __syncthreads();
+    if (ks != 0 || nt >= a.NT_total) return;
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int q = 1; q < KS; ++q) yacc[r] += red[((wave + q) * MR + r) * 64 + lane];
+  }
+
+  const int n = nt * 16 + col;
+  if (n < a.N) {
+    const float b = has_bias ? (BF16 ? oc_bf2f(braw) : oc_h2f(braw)) : 0.f;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      const int m = 4 * kq + r;
+      if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(yacc[r] + b) : oc_f2h(yacc[r] + b);
+    }
+  }
+}
+
 // y[m, n] = sum over splits (in split order) of partial[s, m, n] (+ bias).
 template <bool BF16>
 __global__ void k_splitk_reduce(const float* __restrict__ partial, int S, int M, int N, int N_pad,
-                                const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+                                const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int ldy) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   const int m = blockIdx.y;
   if (n >= N) return;
   float o = 0.f;
   for (int s = 0; s < S; ++s) o += partial[((size_t)s * M + m) * N_pad + n];
   if (bias) o += BF16 ? oc_bf2f(bias[n]) : oc_h2f(bias[n]);
-  y[(size_t)m * N + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
+  y[(size_t)m * ldy + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
 }
 
 // x_perm[m, p] = x[m, perm[p]] (act-order activations, 16-bit elements).
@@ -481,19 +687,74 @@ int dispatch_gemv_bits(int bits, const GemvPlan& p, const GemvArgs& a, hipStream
 }
 
 int launch_reduce(bool bf16, const float* partial, int S, int M, int N, int N_pad, const void* bias,
-                  void* y, hipStream_t st) {
+                  void* y, int ldy, hipStream_t st) {
   const dim3 grid((N + 255) / 256, M);
   if (bf16)
     hipLaunchKernelGGL(k_splitk_reduce<true>, grid, dim3(256), 0, st, partial, S, M, N, N_pad,
-                       (const uint16_t*)bias, (uint16_t*)y);
+                       (const uint16_t*)bias, (uint16_t*)y, ldy);
   else
     hipLaunchKernelGGL(k_splitk_reduce<false>, grid, dim3(256), 0, st, partial, S, M, N, N_pad,
-                       (const uint16_t*)bias, (uint16_t*)y);
+                       (const uint16_t*)bias, (uint16_t*)y, ldy);
   OC_HIP(hipGetLastError());
   return 0;
 }
 
 constexpr int kSkinnyMaxM = 64;
+constexpr size_t kStreamLds = 64 * 1024;
+
+// Waves per n-tile of k_gemv_stream (OC_GEMV_STREAM_KS = 1 or 2; default 2
+// when the units split evenly).
+int stream_ksplit(const oc::Layout& L) {
+  const int e = env_int("OC_GEMV_STREAM_KS", 0);
+  const int ks = (e == 1 || e == 2) ? e : 2;
+  return (L.NU % ks) == 0 ? ks : 1;
+}
+
+size_t stream_lds(const oc::Layout& L, int M) {
+  return (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 16 * 4;
+}
+
+// Units in flight per wave of k_gemv_stream for this layer, or 0 when the
+// layer takes k_gemv: the streaming kernel serves wide layers (at least 1024
+// n-tiles) at M <= 8 whose x fits in 64 KB of LDS and whose groups are
+// powers of two >= 128.  OC_GEMV_STREAM=0 turns it off, =1 forces it where it
+// applies; OC_GEMV_STREAM_D picks the depth (2 or 4).
+int stream_depth(const oc::Layout& L, int M, int gs) {
+  const int e = env_int("OC_GEMV_STREAM", -1);
+  if (e == 0 || M > 8 || gs < 128 || log2_exact(gs) < 0) return 0;
+  if (stream_lds(L, M) > kStreamLds) return 0;
+  if (e != 1 && L.NT < 1024) return 0;
+  const int de = env_int("OC_GEMV_STREAM_D", 0);
+  const int ks = stream_ksplit(L);
+  const int nu = L.NU / ks;
+  int d = (de == 2 || de == 4) ? de : ((nu % 4) == 0 ? 4 : 2);
+  if (de == 0 && (L.bits == 2 || L.bits == 3)) d = 2;  // measured best
+  while (d > 1 && (nu % d) != 0) d /= 2;
+  return d >= 2 && nu >= d ? d : 0;
+}
+
+template <bool BF16>
+int dispatch_stream(int bits, int d, int M, const oc::Layout& L, const StreamArgs& a, hipStream_t st) {
+  const int ks = stream_ksplit(L);
+  const dim3 grid((L.NT * ks + 3) / 4), block(256);
+  size_t lds = stream_lds(L, M);
+  const int mr = M >= 3 ? 4 : M;
+  if (ks > 1 && lds < (size_t)4 * mr * 64 * 4) lds = (size_t)4 * mr * 64 * 4;
+#define OC_ST(B_, D_, MR_)                                                                         \
+  if (bits == B_ && d == D_ && mr == MR_) {                                                        \
+    if (ks == 2) hipLaunchKernelGGL((k_gemv_stream<B_, D_, MR_, 2, BF16>), grid, block, lds, st, a); \
+    else hipLaunchKernelGGL((k_gemv_stream<B_, D_, MR_, 1, BF16>), grid, block, lds, st, a);         \
+    OC_HIP(hipGetLastError());                                                                     \
+    return 0;                                                                                      \
+  }
+#define OC_STB(B_) OC_ST(B_, 2, 1) OC_ST(B_, 2, 2) OC_ST(B_, 2, 4)
+#define OC_STB4(B_) OC_STB(B_) OC_ST(B_, 4, 1) OC_ST(B_, 4, 2) OC_ST(B_, 4, 4)
+  OC_STB4(2) OC_STB4(3) OC_STB4(4) OC_STB4(8)
+#undef OC_STB4
+#undef OC_STB
+#undef OC_ST
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no streaming gemv for bits=%d d=%d", bits, d);
+}
 
 // Tile height of the GEMM for M rows (64 MT rows, 256 columns): see
 // gemm_tile_height; only 256-row tiles for groups that are not multiples of 128.
@@ -539,9 +800,12 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
   return ws;
 }
 
-extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
-                            const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
-                            void* y, void* workspace, size_t ws_bytes, void* stream) {
+namespace {
+
+// y[M, N] (row stride ldy) = x @ dequant(W)^T (+ bias): the body of oc_gptq_gemm.
+int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
+                   const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias, void* y,
+                   int ldy, void* workspace, size_t ws_bytes, hipStream_t st) {
   OC_REQUIRE(bits == 2 || bits == 3 || bits == 4 || bits == 8, OC_ERR_UNSUPPORTED, "unsupported bits=%d", bits);
   OC_REQUIRE(M >= 0 && K > 0 && N > 0, OC_ERR_INVALID, "bad shape M=%d K=%d N=%d", M, K, N);
   OC_REQUIRE(K % 32 == 0, OC_ERR_SHAPE, "K=%d must be a multiple of 32", K);
@@ -551,7 +815,6 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
   const int gs = oc::eff_group(group_size, K);
   OC_REQUIRE(gs % 32 == 0, OC_ERR_UNSUPPORTED, "group_size=%d must be a multiple of 32 (or -1)", group_size);
   const int G = (K + gs - 1) / gs;
-  hipStream_t st = (hipStream_t)stream;
   const oc::Layout L = oc::make_layout(bits, K, N);
   const size_t need = oc_gptq_workspace_bytes(M, K, N, bits, group_size, perm != nullptr);
   OC_REQUIRE(ws_bytes >= need && (need == 0 || workspace), OC_ERR_WORKSPACE,
@@ -567,6 +830,27 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
   }
   const bool bf16 = act_dtype == OC_DTYPE_BF16;
   if (M <= kGemvMaxM) {
+    const int sd = stream_depth(L, M, gs);
+    if (sd > 0) {
+      StreamArgs a;
+      a.x = xa;
+      a.w = (const uint8_t*)packed;
+      a.meta = meta;
+      a.bias = (const uint16_t*)bias;
+      a.y = (uint16_t*)y;
+      a.M = M;
+      a.K = K;
+      a.K_pad = L.K_pad;
+      a.N = N;
+      a.N_pad = L.N_pad;
+      a.NT_total = L.NT;
+      a.NU = L.NU;
+      a.G = G;
+      a.gs = gs;
+      a.gkb_shift = log2_exact(gs) - 7;
+      a.ldy = ldy;
+      return bf16 ? dispatch_stream<true>(bits, sd, M, L, a, st) : dispatch_stream<false>(bits, sd, M, L, a, st);
+    }
     const GemvPlan p = plan_gemv(L, M, gs);
     GemvArgs a;
     a.x = xa;
@@ -586,9 +870,11 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     a.gshift = log2_exact(gs);
     a.S = p.S;
     a.ups = p.ups;
+    a.ldy = ldy;
+    a.bits = bits;
     const int rc = bf16 ? dispatch_gemv_bits<true>(bits, p, a, st) : dispatch_gemv_bits<false>(bits, p, a, st);
     if (rc || p.S == 1) return rc;
-    return launch_reduce(bf16, a.partial, p.S, M, N, L.N_pad, bias, y, st);
+    return launch_reduce(bf16, a.partial, p.S, M, N, L.N_pad, bias, y, ldy, st);
   }
   if (use_gemm(M, L.N_pad, gs)) {
     GemmArgs g;
@@ -612,7 +898,7 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     const GemmPlan gp = plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0), mt);
     g.post = nullptr;
     g.ldx = K;
-    g.ldy = N;
+    g.ldy = ldy;
     g.uk_shift = 0;
     g.pstride = gp.S;
     g.poff = 0;
@@ -667,7 +953,7 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     a.w = (const uint8_t*)packed;
     a.meta = meta;
     a.bias = (const uint16_t*)bias;
-    a.y = (uint16_t*)y + (size_t)m0 * N;
+    a.y = (uint16_t*)y + (size_t)m0 * ldy;
     a.partial = (float*)ws;
     a.M = Mc;
     a.K = K;
@@ -679,9 +965,183 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
     a.gs = gs;
     a.S = p.S;
     a.ups = p.ups;
+    a.ldy = ldy;
     int rc = bf16 ? dispatch_skinny_bits<true>(bits, p, a, st) : dispatch_skinny_bits<false>(bits, p, a, st);
-    if (!rc && p.S > 1) rc = launch_reduce(bf16, a.partial, p.S, Mc, N, L.N_pad, bias, a.y, st);
+    if (!rc && p.S > 1) rc = launch_reduce(bf16, a.partial, p.S, Mc, N, L.N_pad, bias, a.y, ldy, st);
     if (rc) return rc;
   }
   return 0;
+}
+
+}  // namespace
+
+extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
+                            const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
+                            void* y, void* workspace, size_t ws_bytes, void* stream) {
+  return gptq_gemm_impl(x, M, K, N, packed, meta, perm, bits, group_size, act_dtype, bias, y, N, workspace,
+                        ws_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Fused modules: several GPTQ parts (each with its own bits, group size,
+// scales/zeros and act-order permutation) that read the same activations and
+// write side by side into one output.  At M <= 16, when every part has groups
+// of a multiple of 128, one k_gemv_group launch runs all parts; otherwise the
+// parts run one after the other through oc_gptq_gemm's paths.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct GroupPlan {
+  bool fused;
+  int w, xch;
+  size_t lds;
+  size_t perm_off[kMaxParts];  // workspace offset of a part's permuted x
+  size_t bytes;
+};
+
+GroupPlan plan_group(const oc_gptq_part* parts, int n_parts, int M, int K) {
+  GroupPlan g = {};
+  g.fused = M <= kGemvMaxM && n_parts <= kMaxParts;
+  g.w = 16;
+  g.xch = 1;
+  size_t slot = 0, off = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    const oc_gptq_part& P = parts[i];
+    const int gs = oc::eff_group(P.group_size, K);
+    const oc::Layout L = oc::make_layout(P.bits, K, P.N);
+    if ((gs % 128) != 0) g.fused = false;
+    if (g.fused) {
+      const GemvPlan p = plan_gemv(L, M, gs);
+      if (p.S != 1) g.fused = false;
+      g.w = p.w < g.w ? p.w : g.w;
+      g.xch = p.xch > g.xch ? p.xch : g.xch;
+      const size_t sl = (size_t)M * (L.U * 128 + 8) * 2;
+      slot = sl > slot ? sl : slot;
+    }
+    g.perm_off[i < kMaxParts ? i : 0] = off;
+    if (P.perm) off += align256((size_t)M * K * 2);
+  }
+  if (g.fused) {
+    if (g.xch > 1 && g.w > 8) g.w = 8;
+    while (g.w > 4 && slot * g.w > kGemvLds) g.w /= 2;
+    const size_t xb = slot * g.w, rb = (size_t)g.w * 4 * 64 * 4;
+    g.lds = ((xb > rb ? xb : rb) + 15) / 16 * 16;
+    g.bytes = off;
+  } else {  // parts one after the other: they reuse one workspace
+    size_t mx = 0;
+    for (int i = 0; i < n_parts; ++i) {
+      const size_t b = oc_gptq_workspace_bytes(M, K, parts[i].N, parts[i].bits, parts[i].group_size,
+                                               parts[i].perm != nullptr);
+      mx = b > mx ? b : mx;
+    }
+    g.bytes = mx;
+  }
+  return g;
+}
+
+template <bool BF16>
+int launch_group(const GroupPlan& gp, const GemvGroupArgs& ga, int blocks, hipStream_t st) {
+#define OC_GG(W_, XC_)                                                                                \
+  if (gp.w == W_ && gp.xch == XC_) {                                                                  \
+    hipLaunchKernelGGL((k_gemv_group<1, W_, XC_, BF16>), dim3(blocks), dim3(64 * W_), gp.lds, st, ga); \
+    OC_HIP(hipGetLastError());                                                                        \
+    return 0;                                                                                         \
+  }
+  OC_GG(16, 1) OC_GG(8, 1) OC_GG(8, 4) OC_GG(8, 8) OC_GG(8, 16)
+  OC_GG(4, 1) OC_GG(4, 4) OC_GG(4, 8) OC_GG(4, 16)
+#undef OC_GG
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no grouped gemv kernel for w=%d xch=%d", gp.w, gp.xch);
+}
+
+int check_part(const oc_gptq_part& P, int i, int K) {
+  OC_REQUIRE(P.packed && P.meta, OC_ERR_INVALID, "part %d: null pointer", i);
+  OC_REQUIRE(P.bits == 2 || P.bits == 3 || P.bits == 4 || P.bits == 8, OC_ERR_UNSUPPORTED,
+             "part %d: unsupported bits=%d", i, P.bits);
+  OC_REQUIRE(P.N > 0, OC_ERR_INVALID, "part %d: N=%d", i, P.N);
+  const int gs = oc::eff_group(P.group_size, K);
+  OC_REQUIRE(gs % 32 == 0, OC_ERR_UNSUPPORTED, "part %d: group_size=%d must be a multiple of 32 (or -1)", i,
+             P.group_size);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" size_t oc_gptq_grouped_workspace_bytes(const oc_gptq_part* parts, int n_parts, int M, int K) {
+  if (!parts || n_parts < 1 || M <= 0 || K <= 0) return 0;
+  for (int i = 0; i < n_parts; ++i)
+    if (check_part(parts[i], i, K)) return 0;
+  return plan_group(parts, n_parts, M, K).bytes;
+}
+
+extern "C" int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_part* parts, int n_parts,
+                                    int act_dtype, void* y, int ldy, void* workspace, size_t ws_bytes,
+                                    void* stream) {
+  OC_REQUIRE(x && y && parts, OC_ERR_INVALID, "null pointer");
+  OC_REQUIRE(n_parts >= 1, OC_ERR_INVALID, "n_parts=%d", n_parts);
+  OC_REQUIRE(M >= 0 && K > 0, OC_ERR_INVALID, "bad shape M=%d K=%d", M, K);
+  OC_REQUIRE(K % 32 == 0, OC_ERR_SHAPE, "K=%d must be a multiple of 32", K);
+  OC_REQUIRE(act_dtype == OC_DTYPE_F16 || act_dtype == OC_DTYPE_BF16, OC_ERR_UNSUPPORTED, "bad act_dtype %d",
+             act_dtype);
+  int n_total = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    const int rc = check_part(parts[i], i, K);
+    if (rc) return rc;
+    n_total += parts[i].N;
+  }
+  OC_REQUIRE(ldy >= n_total, OC_ERR_SHAPE, "ldy=%d < total width %d", ldy, n_total);
+  if (M == 0) return 0;
+  const GroupPlan gp = plan_group(parts, n_parts, M, K);
+  OC_REQUIRE(ws_bytes >= gp.bytes && (gp.bytes == 0 || workspace), OC_ERR_WORKSPACE,
+             "workspace of %zu bytes is smaller than the %zu required", ws_bytes, gp.bytes);
+  hipStream_t st = (hipStream_t)stream;
+  const bool bf16 = act_dtype == OC_DTYPE_BF16;
+  uint16_t* yo = (uint16_t*)y;
+  if (!gp.fused) {
+    for (int i = 0, off = 0; i < n_parts; off += parts[i].N, ++i) {
+      const oc_gptq_part& P = parts[i];
+      const int rc = gptq_gemm_impl(x, M, K, P.N, P.packed, P.meta, P.perm, P.bits, P.group_size, act_dtype,
+                                    P.bias, yo + off, ldy, workspace, ws_bytes, st);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+  GemvGroupArgs ga = {};
+  int blocks = 0;
+  for (int i = 0, off = 0; i < n_parts; off += parts[i].N, ++i) {
+    const oc_gptq_part& P = parts[i];
+    const int gs = oc::eff_group(P.group_size, K);
+    const oc::Layout L = oc::make_layout(P.bits, K, P.N);
+    const uint16_t* xa = (const uint16_t*)x;
+    if (P.perm) {
+      uint16_t* xp = (uint16_t*)((uint8_t*)workspace + gp.perm_off[i]);
+      hipLaunchKernelGGL(k_gather, dim3((K + 255) / 256, M), dim3(256), 0, st, xa, P.perm, M, K, xp);
+      OC_HIP(hipGetLastError());
+      xa = xp;
+    }
+    GemvArgs& a = ga.part[i];
+    a.x = xa;
+    a.w = (const uint8_t*)P.packed;
+    a.meta = P.meta;
+    a.bias = (const uint16_t*)P.bias;
+    a.y = yo + off;
+    a.partial = nullptr;
+    a.M = M;
+    a.K = K;
+    a.N = P.N;
+    a.N_pad = L.N_pad;
+    a.NT_total = L.NT;
+    a.NU = L.NU;
+    a.G = (K + gs - 1) / gs;
+    a.gs = gs;
+    a.gshift = log2_exact(gs);
+    a.S = 1;
+    a.ups = L.NU;
+    a.ldy = ldy;
+    a.bits = P.bits;
+    ga.block_start[i] = blocks;
+    blocks += L.NT;
+  }
+  for (int i = n_parts; i <= kMaxParts; ++i) ga.block_start[i] = blocks;
+  ga.n_parts = n_parts;
+  return bf16 ? launch_group<true>(gp, ga, blocks, st) : launch_group<false>(gp, ga, blocks, st);
 }

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
-from typing import Dict, Optional
+from typing import Dict, List, Optional
 
 import torch
 
@@ -162,6 +162,54 @@ def gptq_gemm(x: torch.Tensor, prep: PreparedGPTQ, bias: Optional[torch.Tensor] 
            prep.bits, prep.group_size, _DT[x.dtype], _ptr(bias), _ptr(out), _ptr(ws), ws_bytes,
            _stream(dev))
     return out.reshape(*lead, n)
+
+
+class OcGptqPart(ctypes.Structure):
+    _fields_ = [("packed", ctypes.c_void_p), ("meta", ctypes.c_void_p), ("perm", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("N", ctypes.c_int), ("bits", ctypes.c_int),
+                ("group_size", ctypes.c_int)]
+
+
+def gptq_gemm_grouped(x: torch.Tensor, preps: List[PreparedGPTQ],
+                      biases: Optional[List[Optional[torch.Tensor]]] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Parts of a fused module side by side: y[..., off_p:off_p+N_p] = x @ dequant(W_p)^T (+ b_p).
+
+    The parts may differ in bits, group size and act-order (oc_gptq_gemm_grouped).
+    """
+    if not 1 <= len(preps) <= 8:
+        raise ValueError(f"{len(preps)} parts; 1..8 are supported")
+    dev = preps[0].packed.device
+    if x.dtype not in _DT:
+        raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
+    k = preps[0].in_features
+    if any(p.in_features != k for p in preps):
+        raise ValueError("all parts of a fused module must have the same in_features")
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} features, layer expects {k}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    _need(x2, "x", x.dtype, dev=dev)
+    m = x2.shape[0]
+    n_total = sum(p.out_features for p in preps)
+    if out is None:
+        out = torch.empty((m, n_total), dtype=x.dtype, device=dev)
+    else:
+        _need(out, "out", x.dtype, (m, n_total), dev)
+    arr = (OcGptqPart * len(preps))()
+    for i, p in enumerate(preps):
+        b = None if biases is None else biases[i]
+        if b is not None:
+            _need(b, "bias", x.dtype, (p.out_features,), dev)
+        arr[i] = OcGptqPart(p.packed.data_ptr(), p.meta.data_ptr(), _ptr(p.perm), _ptr(b), p.out_features,
+                            p.bits, p.group_size)
+    ws_bytes = N.load().oc_gptq_grouped_workspace_bytes(arr, len(preps), m, k)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    N.call("oc_gptq_gemm_grouped", _ptr(x2), m, k, arr, len(preps), _DT[x.dtype], _ptr(out), n_total,
+           _ptr(ws), ws_bytes, _stream(dev))
+    return out.reshape(*lead, n_total)
 
 
 # ---------------------------------------------------------------------------------- Hadamard

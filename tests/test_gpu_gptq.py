@@ -247,3 +247,26 @@ def test_gemm_split_tail(dev, monkeypatch, dtype):
     ref = og.linear_ref(xb, w, dtype, bb)
     r = _rel(_np(y[:, n0:n1].float()), ref)
     assert r <= 1e-2, f"max rel err {r:.3e}"
+
+
+# Wide layers at M <= 8 take the streaming GEMV (one wave per n-tile, x staged in LDS):
+# every bit width, partial last workgroup (N not a multiple of 64 columns), bias, act-order, bf16.
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+def test_gemm_streaming_wide(dev, bits, m):
+    n = 16384 + 48 if bits != 3 else 16384 + 32  # >= 1024 n-tiles, last workgroup partial
+    _gemm_check(dev, _case(512, n, bits, seed=60 + bits + m), m, "fp16", bias=(m == 3))
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("case", ["act", "bf16", "g256", "narrow_forced"])
+def test_gemm_streaming_variants(dev, bits, case, monkeypatch):
+    if case == "act":
+        _gemm_check(dev, _case(1024, 16384, bits, 128, True, seed=70 + bits), 2, "fp16", bias=True)
+    elif case == "bf16":
+        _gemm_check(dev, _case(512, 16384, bits, seed=80 + bits), 4, "bf16", bias=True)
+    elif case == "g256":
+        _gemm_check(dev, _case(1024, 16384, bits, 256, False, seed=90 + bits), 1, "fp16")
+    else:  # forced on a narrow layer: fewer n-tiles than one workgroup's 4 waves in the last group
+        monkeypatch.setenv("OC_GEMV_STREAM", "1")
+        _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=95 + bits), 5, "fp16", bias=True)
