@@ -35,6 +35,7 @@ import torch
 from . import ops
 from . import _native as N
 from .module_utils import (
+    constituent_configs,
     lookup_module_config,
     parse_layer_and_module,
     validate_quant_config_within_shard,
@@ -187,6 +188,126 @@ class GPTQLinearMethod(LinearMethodBase):
         return ops.gptq_gemm(x, prep, bias)
 
 
+class MixedFusedGPTQLinearMethod(LinearMethodBase):
+    """A fused module (qkv_proj, gate_up_proj) whose shards differ in bits or group size.
+
+    The reference rejects such modules (vllm_plugins/gptq/vllm_plugin.py:310-317 via
+    utils/module.py:153-177); with ``fused_mixed_bits`` enabled in the quantization config they
+    are served as one ``apply()`` that runs every shard in one launch
+    (``oc_gptq_gemm_grouped``).  Each checkpoint tensor of shard i (``q_proj.qweight`` etc.,
+    AutoGPTQ layout at that shard's bits) is stored flat, back to back, in one parameter of the
+    fused name, because the shards' packed shapes differ; ``g_idx`` is [n_shards, K].
+    """
+
+    def __init__(self, part_configs: List[GPTQLayerConfig]):
+        self.part_configs = part_configs
+
+    def create_weights(self, layer: torch.nn.Module, input_size_per_partition: int,
+                       output_partition_sizes: List[int], input_size: int, output_size: int,
+                       params_dtype: torch.dtype, **extra_weight_attrs):
+        k = input_size_per_partition
+        if len(output_partition_sizes) != len(self.part_configs):
+            raise ValueError(f"{len(output_partition_sizes)} output partitions for "
+                             f"{len(self.part_configs)} shard configs")
+        if k % 32:
+            raise ValueError(f"input size {k} must be a multiple of 32 for GPTQ packing")
+        extra_weight_attrs.pop("weight_loader", None)
+        shapes = {"qweight": [], "qzeros": [], "scales": []}
+        groups = []
+        for n, cfg in zip(output_partition_sizes, self.part_configs):
+            b = cfg.weight_bits
+            gs = cfg.group_size if cfg.group_size != -1 else input_size
+            if (n * b) % 32 or gs % 32:
+                raise ValueError(f"shard of {n} outputs at {b} bits / group {cfg.group_size} does not pack")
+            g = (k + gs - 1) // gs
+            groups.append(g)
+            shapes["qweight"].append((k * b // 32, n))
+            shapes["qzeros"].append((g, n * b // 32))
+            shapes["scales"].append((g, n))
+        n_shards = len(self.part_configs)
+
+        def flat_param(name, dtype):
+            offs, c = [], 0
+            for shp in shapes[name]:
+                offs.append(c)
+                c += shp[0] * shp[1]
+            prm = torch.nn.Parameter(torch.empty(c, dtype=dtype), requires_grad=False)
+
+            def _load(param, loaded_weight: torch.Tensor, loaded_shard_id: Any = None):
+                if loaded_shard_id is None:
+                    raise ValueError(f"{name} of a fused module with per-shard bits needs a shard id")
+                i = _shard_index(loaded_shard_id, n_shards)
+                shp = shapes[name][i]
+                if tuple(loaded_weight.shape) != shp:
+                    raise ValueError(f"{name} shard {loaded_shard_id}: got {tuple(loaded_weight.shape)}, "
+                                     f"expected {shp}")
+                param.data[offs[i]:offs[i] + shp[0] * shp[1]].view(shp).copy_(loaded_weight)
+
+            set_weight_attrs(prm, {"weight_loader": _load, "oc_shard_offsets": offs,
+                                   "oc_shard_shapes": shapes[name], **extra_weight_attrs})
+            return prm
+
+        g_idx = torch.nn.Parameter(torch.stack([
+            torch.tensor([i // (c.group_size if c.group_size != -1 else input_size) for i in range(k)],
+                         dtype=torch.int32) for c in self.part_configs]), requires_grad=False)
+
+        def _g_load(param, loaded_weight: torch.Tensor, loaded_shard_id: Any = None):
+            if loaded_shard_id is None:
+                param.data.copy_(loaded_weight.reshape(1, -1).expand_as(param.data))
+                return
+            param.data[_shard_index(loaded_shard_id, n_shards)].copy_(loaded_weight)
+
+        set_weight_attrs(g_idx, {"weight_loader": _g_load, "ignore_warning": True, **extra_weight_attrs})
+        layer.register_parameter("qweight", flat_param("qweight", torch.int32))
+        layer.register_parameter("g_idx", g_idx)
+        layer.register_parameter("qzeros", flat_param("qzeros", torch.int32))
+        layer.register_parameter("scales", flat_param("scales", torch.float16))
+        layer._oc_gptq = {"in": k, "out": sum(output_partition_sizes), "parts": list(output_partition_sizes),
+                          "groups": groups}
+
+    def shard_tensors(self, layer: torch.nn.Module, i: int):
+        """(qweight, qzeros, scales, g_idx) views of shard i."""
+        out = []
+        for name in ("qweight", "qzeros", "scales"):
+            p = getattr(layer, name)
+            off, shp = p.oc_shard_offsets[i], p.oc_shard_shapes[i]
+            out.append(p.data[off:off + shp[0] * shp[1]].view(shp))
+        out.append(layer.g_idx.data[i])
+        return out
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        dev = layer.qweight.device
+        if dev.type != "cuda":
+            raise RuntimeError("MixedFusedGPTQLinearMethod needs the layer on a HIP device before "
+                               "process_weights_after_loading")
+        preps = []
+        for i, cfg in enumerate(self.part_configs):
+            qw, qz, sc, g_idx = self.shard_tensors(layer, i)
+            g_idx = g_idx.to(torch.int32).contiguous()
+            if not cfg.desc_act:
+                gs = cfg.group_size if cfg.group_size != -1 else layer._oc_gptq["in"]
+                expected = torch.arange(g_idx.numel(), device=dev, dtype=torch.int32) // gs
+                if torch.equal(g_idx, expected):
+                    g_idx = None
+            preps.append(ops.gptq_prepare(qw.contiguous(), qz.contiguous(), sc.to(torch.float16).contiguous(),
+                                          g_idx, cfg.weight_bits, cfg.group_size, cfg.zero_format))
+        layer._oc_preps = preps
+
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor,
+              bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        preps = getattr(layer, "_oc_preps", None)
+        if preps is None:
+            raise RuntimeError("GPTQ layer used before process_weights_after_loading")
+        biases = None
+        if bias is not None:
+            b = bias.to(x.dtype) if bias.dtype != x.dtype else bias
+            biases, off = [], 0
+            for p in preps:
+                biases.append(b[off:off + p.out_features])
+                off += p.out_features
+        return ops.gptq_gemm_grouped(x, preps, biases)
+
+
 def _zero_loader(loader, offs, parts, bits):
     """qzeros are packed along N: shard i occupies columns offs[i]*b/32 ..."""
     if loader is not None:
@@ -209,8 +330,11 @@ class MixedGPTQConfig(QuantizationConfig):
 
     def __init__(self, quantization_bits, group_size=-1, desc_act=False, sym=False,
                  lm_head_quantized=False, checkpoint_format="gptq_v2",
-                 rotation_metadata: Optional[RotationMetadata] = None):
+                 rotation_metadata: Optional[RotationMetadata] = None, fused_mixed_bits: bool = False):
         super().__init__()
+        # Extension (off by default, as in the reference): serve fused modules whose shards
+        # differ in bits or group size instead of raising ValueError.
+        self.fused_mixed_bits = bool(fused_mixed_bits)
         self.quantization_bits = quantization_bits
         self.group_size = group_size
         self.desc_act = desc_act
@@ -257,7 +381,8 @@ class MixedGPTQConfig(QuantizationConfig):
                    sym=config.get("sym", False),
                    lm_head_quantized=config.get("lm_head", False),
                    checkpoint_format=config.get("checkpoint_format", "gptq_v2"),
-                   rotation_metadata=RotationMetadata.from_quant_config(config))
+                   rotation_metadata=RotationMetadata.from_quant_config(config),
+                   fused_mixed_bits=config.get("fused_mixed_bits", False))
 
     def maybe_update_config(self, model_name, hf_config=None, revision=None):
         """No-op: per-module dispatch comes from ``quantization_bits`` (vllm_plugin.py:213-218)."""
@@ -271,6 +396,23 @@ class MixedGPTQConfig(QuantizationConfig):
             if isinstance(extra, dict) and extra.get("group_size") is not None:
                 return extra["group_size"]
         return self.group_size
+
+    def _mixed_fused_method(self, layer_idx: int, suffix: str, prefix: str):
+        """MixedFusedGPTQLinearMethod when enabled and every shard is a GPTQ entry, else None."""
+        if not self.fused_mixed_bits:
+            return None
+        cfgs = constituent_configs(self.quantization_bits, layer_idx, suffix)
+        if not cfgs or any(c is None for c in cfgs):
+            return None
+        parts = []
+        for c in cfgs:
+            bits = int(c.get("bits", 0))
+            if c.get("method", "gptq") != "gptq" or bits not in SUPPORTED_BITS:
+                return None
+            parts.append(GPTQLayerConfig(bits, self.resolve_group_size(c), self.desc_act, bool(self.sym),
+                                         self.checkpoint_format))
+        return maybe_wrap_rotation_method(MixedFusedGPTQLinearMethod(parts), prefix=prefix,
+                                          metadata=self.rotation_metadata)
 
     def _unquantized(self, prefix: str):
         return maybe_wrap_rotation_method(UnquantizedLinearMethod(), prefix=prefix,
@@ -290,6 +432,9 @@ class MixedGPTQConfig(QuantizationConfig):
         if mod_cfg is None:
             return self._unquantized(prefix)
         if not validate_quant_config_within_shard(self.quantization_bits, layer_idx, suffix):
+            mixed = self._mixed_fused_method(layer_idx, suffix, prefix)
+            if mixed is not None:
+                return mixed
             raise ValueError(f"Detected some but not all shards of {prefix} are quantized. "
                              "All shards of fused layers to have the same precision.")
         bits = mod_cfg.get("bits", 0)

@@ -59,3 +59,32 @@ def test_act_order_down_proj_layer(dev, bits):
     y = layer(x.to(dev)).float().cpu().numpy()
     ref = _ref([c], x.numpy())
     assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) <= 1e-2
+
+
+@pytest.mark.parametrize("v_gs,act,m", [(128, False, 1), (128, True, 4), (64, False, 3), (128, False, 40)])
+def test_fused_qkv_mixed_bits_layer(dev, v_gs, act, m):
+    """fused_mixed_bits: q@4b, k/v@8b served as one qkv_proj (one launch when every group is a
+    multiple of 128 and M <= 16, shard by shard otherwise), with bias, vs the oracle."""
+    qb = [{"self_attn.q_proj": {"bits": 4, "method": "gptq", "group_size": 128},
+           "self_attn.k_proj": {"bits": 8, "method": "gptq", "group_size": 128},
+           "self_attn.v_proj": {"bits": 8, "method": "gptq", "group_size": v_gs}}]
+    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": qb, "checkpoint_format": "gptq",
+                                         "desc_act": act, "fused_mixed_bits": True})
+    parts, k = [512, 128, 128], 1024
+    layer = LinearBase(k, sum(parts), bias=True, quant_config=cfg, prefix="model.layers.0.self_attn.qkv_proj",
+                       output_partition_sizes=parts)
+    assert isinstance(layer.quant_method, G.MixedFusedGPTQLinearMethod)
+    cases = [synth.gptq_case(s, k, n, b, gs, act, seed=i)
+             for i, (s, n, b, gs) in enumerate(zip("qkv", parts, (4, 8, 8), (128, 128, v_gs)))]
+    for c, sid in zip(cases, "qkv"):
+        for name in ("qweight", "qzeros", "scales") + (("g_idx",) if act else ()):
+            p = getattr(layer, name)
+            p.weight_loader(p, getattr(c, name), sid)
+    bias = (torch.randn(sum(parts), generator=torch.Generator().manual_seed(2)) * 0.1).half()
+    layer.bias.data.copy_(bias)
+    layer.to(dev)
+    layer.quant_method.process_weights_after_loading(layer)
+    x = synth.activations(m, k, seed=9)
+    y = layer(x.to(dev)).float().cpu().numpy()
+    ref = _ref(cases, x.numpy()) + bias.float().numpy()
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) <= 1e-2

@@ -159,3 +159,48 @@ def test_fused_weight_loader_places_shards():
         assert torch.equal(layer.qweight.data[:, off:off + n], qw)
         assert torch.equal(layer.qzeros.data[:, off * bits // 32:(off + n) * bits // 32], qz)
         off += n
+
+
+MIXED_QKV = [{"self_attn.q_proj": {"bits": 4, "method": "gptq", "group_size": 128},
+              "self_attn.k_proj": {"bits": 8, "method": "gptq", "group_size": 128},
+              "self_attn.v_proj": {"bits": 8, "method": "gptq", "group_size": 64}}]
+
+
+def test_fused_mixed_bits_is_opt_in():
+    """Default: the reference's ValueError; with fused_mixed_bits: one method over all shards."""
+    with pytest.raises(ValueError, match="All shards of fused layers"):
+        G.MixedGPTQConfig.from_config({"quantization_bits": MIXED_QKV}).get_quant_method(
+            _layer(), "model.layers.0.self_attn.qkv_proj")
+    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": MIXED_QKV, "fused_mixed_bits": True})
+    m = cfg.get_quant_method(_layer(), "model.layers.0.self_attn.qkv_proj")
+    assert isinstance(m, G.MixedFusedGPTQLinearMethod)
+    assert [(c.weight_bits, c.group_size) for c in m.part_configs] == [(4, 128), (8, 128), (8, 64)]
+    # a missing shard still raises
+    partial = [{"mlp.gate_proj": {"bits": 4}}]
+    with pytest.raises(ValueError):
+        G.MixedGPTQConfig.from_config({"quantization_bits": partial, "fused_mixed_bits": True}).get_quant_method(
+            _layer(), "model.layers.0.mlp.gate_up_proj")
+
+
+def test_fused_mixed_bits_loaders_place_shards():
+    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": MIXED_QKV, "fused_mixed_bits": True})
+    m = cfg.get_quant_method(_layer(), "model.layers.0.self_attn.qkv_proj")
+    layer = torch.nn.Module()
+    k, parts = 256, [64, 32, 32]
+    m.create_weights(layer, k, parts, k, sum(parts), torch.float16)
+    loaded = {}
+    for i, (sid, n, b, gs) in enumerate(zip("qkv", parts, (4, 8, 8), (128, 128, 64))):
+        g = k // gs
+        qw = torch.randint(-2**31, 2**31 - 1, (k * b // 32, n), dtype=torch.int32)
+        qz = torch.randint(-2**31, 2**31 - 1, (g, n * b // 32), dtype=torch.int32)
+        sc = torch.rand(g, n).half()
+        gi = torch.randperm(k).to(torch.int32) // gs
+        for name, t in (("qweight", qw), ("qzeros", qz), ("scales", sc), ("g_idx", gi)):
+            p = getattr(layer, name)
+            p.weight_loader(p, t, sid)
+        loaded[i] = (qw, qz, sc, gi)
+        with pytest.raises(ValueError):
+            layer.qweight.weight_loader(layer.qweight, qw[:, :1], sid)
+    for i in range(3):
+        for got, want in zip(m.shard_tensors(layer, i), loaded[i]):
+            assert torch.equal(got, want)
