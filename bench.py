@@ -2,10 +2,11 @@
 
 Default workload: one Llama-3-8B decoder layer's seven
 Mixed-GPTQ projections (q/o 4-bit, k/v 8-bit, gate/up 3-bit, down 2-bit,
-group 128) at M = 1 with fp16 activations.  A step = the layer's
-``GPTQLinearMethod.apply`` calls over one batch: k|v and gate|up are merged
-layers (same input, same bits: one apply, one launch each, as vLLM builds
-them), q, o and down are single -- 5 launches.
+group 128) at M = 1 with fp16 activations.  A step = the layer's apply()
+calls over one batch as a fused-module plugin issues them: qkv_proj is one
+fused module whose shards differ in bits (q 4-bit | k, v 8-bit, served with
+``fused_mixed_bits`` by one grouped launch), gate|up is a merged same-bits
+layer, o and down are single -- 4 launches.
 
 - value: whole-step algorithmic bytes (packed weights + fp16 scales + packed
   zeros + x + y, each counted once) / wall time per step, with all inputs
@@ -60,21 +61,40 @@ def _prepare_copies(cases, dev, min_bytes):
     return sets
 
 
+def _call_name(call):
+    if len(call) == 1:
+        return call[0].name
+    return "qkv_proj" if call[0].name == "q_proj" else "+".join(c.name for c in call)
+
+
 def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes=1 << 30):
     import torch
 
     from onecompression_amd import ops, synth
 
     dtype = torch.float16 if dtype_name == "fp16" else torch.bfloat16
-    cases = synth.layer_cases(cfg)
-    sets = _prepare_copies(cases, dev, rotate_bytes)
-    xs = [synth.activations(m, c.in_features, dtype, seed=100 + i).to(dev) for i, c in enumerate(cases)]
-    outs = [torch.empty((m, c.out_features), dtype=dtype, device=dev) for c in cases]
-    step_bytes = sum(_gptq_bytes(c, m) for c in cases)
+    calls = synth.layer_calls(cfg)
+    cases = [c for call in calls for c in call]
+    flat = _prepare_copies(cases, dev, rotate_bytes)
+    # per copy: the prepared parts of each call
+    sets = []
+    for preps in flat:
+        it = iter(preps)
+        sets.append([[next(it) for _ in call] for call in calls])
+    xs = [synth.activations(m, call[0].in_features, dtype, seed=100 + i).to(dev) for i, call in enumerate(calls)]
+    outs = [torch.empty((m, sum(c.out_features for c in call)), dtype=dtype, device=dev) for call in calls]
+    step_bytes = sum(_gptq_bytes(c, m) - (2 * m * c.in_features if j else 0)
+                     for call in calls for j, c in enumerate(call))  # x read once per call
+
+    def launch(j, preps):
+        if len(preps) == 1:
+            ops.gptq_gemm(xs[j], preps[0], out=outs[j])
+        else:
+            ops.gptq_gemm_grouped(xs[j], preps, out=outs[j])
 
     def step(i):
-        for p, x, o in zip(sets[i % len(sets)], xs, outs):
-            ops.gptq_gemm(x, p, out=o)
+        for j, preps in enumerate(sets[i % len(sets)]):
+            launch(j, preps)
 
     for i in range(max(warmup, len(sets))):
         step(i)
@@ -96,26 +116,26 @@ def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
 
-    # Per-kernel durations: for each projection, HIP events on the launch
-    # stream around `steps` back-to-back launches of that kernel (rotating
+    # Per-call durations: for each apply() call, HIP events on the launch
+    # stream around `steps` back-to-back launches of that call (rotating
     # weight copies), with the stream pre-loaded by a spin kernel so that the
     # host enqueues every launch before the GPU reaches them.
-    per_kernel_ms = []
     torch.cuda._sleep(int(1e8))
     evs = []
-    for j in range(len(cases)):
+    for j in range(len(calls)):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for i in range(steps):
-            ops.gptq_gemm(xs[j], sets[(warmup + i) % len(sets)][j], out=outs[j])
+            launch(j, sets[(warmup + i) % len(sets)][j])
         e1.record()
         evs.append((e0, e1))
     torch.cuda.synchronize()
     per_kernel_ms = [e0.elapsed_time(e1) / steps for e0, e1 in evs]
     kernels = []
-    for c, t in zip(cases, per_kernel_ms):
-        b = _gptq_bytes(c, m)
-        kernels.append({"name": c.name, "bits": c.bits, "K": c.in_features, "N": c.out_features,
+    for call, t in zip(calls, per_kernel_ms):
+        b = sum(_gptq_bytes(c, m) - (2 * m * c.in_features if j else 0) for j, c in enumerate(call))
+        kernels.append({"name": _call_name(call), "bits": "|".join(str(c.bits) for c in call),
+                        "K": call[0].in_features, "N": sum(c.out_features for c in call),
                         "bytes": b, "us": t * 1e3, "GBps": b / (t * 1e-3) / 1e9})
     return {"step_bytes": step_bytes, "wall_s": wall, "kernels": kernels, "copies": len(sets),
             "cases": cases}
@@ -417,7 +437,7 @@ def main():
     r = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev)
     dom = max(r["kernels"], key=lambda k: k["us"])
     value = r["step_bytes"] / r["wall_s"] / 1e9
-    kname = f"k_gemv {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b"
+    kname = f"k_gemv_stream {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b"
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
@@ -437,8 +457,9 @@ def main():
         "dtype": "fp16",
         "data": "synthetic (seeded uniform codes/zeros, |N(0,0.02)|+1e-3 scales, N(0,1) x)",
         "config": {"workload": f"cfg{args.config} Llama-3-8B decoder layer, 7 Mixed-GPTQ projections "
-                               f"(q,o 4b; k,v 8b; gate,up 3b; down 2b; gs128) as 5 apply() calls "
-                               f"(k|v and gate|up merged as vLLM does), M={args.m}, fp16",
+                               f"(q,o 4b; k,v 8b; gate,up 3b; down 2b; gs128) as 4 apply() calls: "
+                               f"qkv_proj (q 4b | k,v 8b in one grouped launch), o_proj, gate_up_proj, "
+                               f"down_proj, M={args.m}, fp16",
                    "M": args.m, "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
                    "weight_copies_rotated": r["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS,

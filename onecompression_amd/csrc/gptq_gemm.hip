@@ -702,11 +702,11 @@ int launch_reduce(bool bf16, const float* partial, int S, int M, int N, int N_pa
 constexpr int kSkinnyMaxM = 64;
 constexpr size_t kStreamLds = 64 * 1024;
 
-// Waves per n-tile of k_gemv_stream (OC_GEMV_STREAM_KS = 1 or 2; default 2
-// when the units split evenly).
+// Waves per n-tile of k_gemv_stream (OC_GEMV_STREAM_KS = 1 or 2; default 1,
+// measured faster than two half-K waves on the configs' wide layers).
 int stream_ksplit(const oc::Layout& L) {
   const int e = env_int("OC_GEMV_STREAM_KS", 0);
-  const int ks = (e == 1 || e == 2) ? e : 2;
+  const int ks = (e == 1 || e == 2) ? e : 1;
   return (L.NU % ks) == 0 ? ks : 1;
 }
 

@@ -125,6 +125,19 @@ def layer_cases(cfg: int, seed: int = 0):
     return out
 
 
+def layer_calls(cfg: int, seed: int = 0):
+    """The apply() calls of one decoder layer as a fused-module plugin issues them: a list of
+    calls, each a list of parts.  Same-bits shards are merged into one part (vLLM's merged
+    layers); a call with several parts is a fused module whose shards differ in bits
+    (q@4b with k, v@8b as one qkv_proj, served by oc_gptq_gemm_grouped)."""
+    if cfg != 1:
+        return [[c] for c in layer_cases(cfg, seed)]
+    by_name = {c.name: c for c in config_cases(cfg, seed)}
+    kv = fuse_cases([by_name["k_proj"], by_name["v_proj"]], "k_v_proj")
+    gu = fuse_cases([by_name["gate_proj"], by_name["up_proj"]], "gate_up_proj")
+    return [[by_name["q_proj"], kv], [by_name["o_proj"]], [gu], [by_name["down_proj"]]]
+
+
 def config_cases(cfg: int, seed: int = 0):
     spec = {0: CONFIG0, 1: CONFIG1, 2: CONFIG2, 4: CONFIG4}[cfg]
     act = cfg == 2
