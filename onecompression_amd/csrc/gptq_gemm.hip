@@ -520,6 +520,150 @@ __global__ __launch_bounds__(256, 4) void k_gemv_stream(const StreamArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide layers at mid M (up to 64 rows): the same one-wave-per-n-tile stream
+// over K, with x staged one k-block (128 k) at a time in a two-buffer LDS
+// ring shared by the workgroup's 4 waves, one barrier per k-block.  Each
+// decoded B operand feeds MB = ceil(M / 16) MFMAs (the 16-row blocks of x).
+// The staging loads of k-block kb + 2 are issued while kb is computed; the
+// rows' sums over each k-block (for the zero-point correction) are formed
+// from the staged registers with a 16-lane butterfly, once per workgroup.
+// ---------------------------------------------------------------------------
+template <int BITS, int MB, bool BF16>
+__global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
+  using GG = Geo<BITS>;
+  constexpr int U = GG::U, P = GG::P;
+  constexpr int D = 2;        // units in flight per wave
+  constexpr int XLD = 136;    // halfs per staged row (128 + 8 pad)
+  constexpr int ROWS = 16 * MB;
+  constexpr float OFF = dec_offset<BITS, BF16>();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, kq = lane >> 4;
+  const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<BF16>());
+  const int nt = blockIdx.x * 4 + wave;
+  const int ntc = min(nt, a.NT_total - 1);  // waves past the last n-tile compute it, unused
+  const int M = a.M;
+
+  extern __shared__ __align__(16) uint16_t xl[];   // [2][ROWS][XLD]
+  float* xsum = (float*)(xl + 2 * ROWS * XLD);     // [2][ROWS]
+
+  // staging of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at 8 (c % 16))
+  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.x, (uint32_t)M * a.K * 2);
+  oc_u4 xs_reg[MB];
+  auto stage_load = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int c = threadIdx.x + 256 * j, row = c >> 4, k = kb * 128 + 8 * (c & 15);
+      xs_reg[j] = oc_bload16(xr, row < M && k < a.K ? (uint32_t)(row * a.K + k) * 2 : kOcOob);
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int c = threadIdx.x + 256 * j, row = c >> 4;
+      *(oc_u4*)(xl + (buf * ROWS + row) * XLD + 8 * (c & 15)) = xs_reg[j];
+      float sum = 0.f;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t pr = xs_reg[j][h];
+        sum += (BF16 ? oc_bf2f((uint16_t)(pr & 0xFFFFu)) : oc_h2f((uint16_t)(pr & 0xFFFFu))) +
+               (BF16 ? oc_bf2f((uint16_t)(pr >> 16)) : oc_h2f((uint16_t)(pr >> 16)));
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+      if ((c & 15) == 0) xsum[buf * ROWS + row] = sum;
+    }
+  };
+
+  const bool has_bias = a.bias != nullptr;
+  const uint16_t braw = __builtin_amdgcn_raw_buffer_load_b16(
+      oc_rsrc(a.bias, (uint32_t)a.N * 2), has_bias && nt * 16 + col < a.N ? (uint32_t)(nt * 16 + col) * 2 : kOcOob,
+      0, 0);
+  const __amdgpu_buffer_rsrc_t wr = oc_rsrc(a.w + (size_t)ntc * a.NU * P * 1024, (uint32_t)a.NU * P * 1024);
+  const __amdgpu_buffer_rsrc_t mr = oc_rsrc(a.meta, (uint32_t)a.G * a.N_pad * 4);
+  const uint32_t mcol = (uint32_t)(ntc * 16 + col) * 4;
+  uint32_t wb[D][4 * P];
+  uint32_t mb[D][U];
+  auto load = [&](int u, uint32_t (&w)[4 * P], uint32_t (&m)[U]) {
+#pragma unroll
+    for (int pt = 0; pt < P; ++pt) {
+      const oc_u4 v = oc_bload16_nt(wr, (uint32_t)(u * P + pt) * 1024 + lane * 16);
+      w[4 * pt] = v[0];
+      w[4 * pt + 1] = v[1];
+      w[4 * pt + 2] = v[2];
+      w[4 * pt + 3] = v[3];
+    }
+#pragma unroll
+    for (int kbl = 0; kbl < U; ++kbl) {
+      const int g = (u * U + kbl) >> a.gkb_shift;
+      m[kbl] = __builtin_amdgcn_raw_buffer_load_b32(mr, mcol + (uint32_t)(g * a.N_pad) * 4, 0, 0);
+    }
+  };
+  oc_f4 yacc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) yacc[i] = oc_f4{0.f, 0.f, 0.f, 0.f};
+  const int nkb = a.NU * U;
+  // k-block kb: x from buffer kb & 1; afterwards the staged registers of
+  // kb + 1 go to the other buffer, kb + 2 is loaded, one barrier.
+  auto consume = [&](int u, const uint32_t (&w)[4 * P], const uint32_t (&m)[U]) {
+#pragma unroll
+    for (int kbl = 0; kbl < U; ++kbl) {
+      const int kb = u * U + kbl, buf = kb & 1;
+      oc_u4 bq[4];
+      decode_kblock<BITS, BF16>(w, kbl, bq, msk, mag);
+      const uint32_t md = m[kbl];
+      const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
+      const float oz = OFF + (float)(md >> 16);
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const uint16_t* arow = xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq;
+        oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(*(const oc_u4*)(arow + 32 * t), bq[t], acc);
+        const oc_f4 xsv = *(const oc_f4*)(xsum + buf * ROWS + 16 * i + 4 * kq);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yacc[i][r] = fmaf(sc, fmaf(-oz, xsv[r], acc[r]), yacc[i][r]);
+      }
+      stage_store(buf ^ 1);               // k-block kb + 1 (its buffer was last read at kb - 1)
+      stage_load(min(kb + 2, nkb - 1));   // past the end: reload the last k-block, unused
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);  // one k-block's decode at a time (register pressure)
+    }
+  };
+  // prologue: x of k-blocks 0 (to LDS) and 1 (in registers), D weight units
+  stage_load(0);
+  stage_store(0);
+  stage_load(min(1, nkb - 1));
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load(d, wb[d], mb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();
+  for (int i0 = 0; i0 < a.NU - D; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(i0 + d, wb[d], mb[d]);
+      load(i0 + D + d, wb[d], mb[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) consume(a.NU - D + d, wb[d], mb[d]);
+
+  const int n = nt * 16 + col;
+  if (nt < a.NT_total && n < a.N) {
+    const float b = has_bias ? (BF16 ? oc_bf2f(braw) : oc_h2f(braw)) : 0.f;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + 4 * kq + r;
+        if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(yacc[i][r] + b) : oc_f2h(yacc[i][r] + b);
+      }
+  }
+}
+
 // y[m, n] = sum over splits (in split order) of partial[s, m, n] (+ bias).
 template <bool BF16>
 __global__ void k_splitk_reduce(const float* __restrict__ partial, int S, int M, int N, int N_pad,
@@ -629,6 +773,7 @@ GemvPlan plan_gemv(const oc::Layout& L, int M, int gs) {
   if (w != 4 && w != 8 && w != 16) w = (p.ngroups >= 512 || p.nt == 2) ? 8 : 16;
   if (p.cs == 1 && w == 16) w = 8;
   if (p.xch > 1 && w == 16) w = 8;
+  if (p.xch == 16) w = 4;  // the 16-chunk x ring is built for 4 waves only
   const size_t slot = (size_t)M * (L.U * 128 + 8) * 2;
   while (w > 4 && slot * w > kGemvLds) w /= 2;
   p.w = w;
@@ -700,7 +845,7 @@ int launch_reduce(bool bf16, const float* partial, int S, int M, int N, int N_pa
 }
 
 constexpr int kSkinnyMaxM = 64;
-constexpr size_t kStreamLds = 64 * 1024;
+constexpr size_t kStreamLds = 80 * 1024;  // two workgroups per CU (160 KB of LDS)
 
 // Waves per n-tile of k_gemv_stream (OC_GEMV_STREAM_KS = 1 or 2; default 1,
 // measured faster than two half-K waves on the configs' wide layers).
@@ -714,14 +859,43 @@ size_t stream_lds(const oc::Layout& L, int M) {
   return (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 16 * 4;
 }
 
+// k_gemm_stream serves wide layers (at least 1024 n-tiles) at 12 < M <= 32
+// (and M <= 12 when x does not fit k_gemv_stream's LDS) with groups that are
+// powers of two >= 128 and an even number of units.  OC_GEMM_STREAM=0 turns
+// it off, =1 forces it where it applies.
+bool use_gemm_stream(const oc::Layout& L, int M, int gs) {
+  const int e = env_int("OC_GEMM_STREAM", -1);
+  if (e == 0 || M > 32 || gs < 128 || log2_exact(gs) < 0 || (L.NU % 2) != 0) return false;
+  if (e == 1) return true;
+  // measured: k_gemv is faster for 4 < M <= 12, the streaming GEMM from 13 rows
+  return L.NT >= 1024 && (M > 12 || (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 64 > 80 * 1024);
+}
+
+template <bool BF16>
+int dispatch_gemm_stream(int bits, int M, const oc::Layout& L, const StreamArgs& a, hipStream_t st) {
+  const int mbt = M <= 16 ? 1 : 2;
+  const dim3 grid((L.NT + 3) / 4), block(256);
+  const size_t lds = (size_t)2 * 16 * mbt * 136 * 2 + (size_t)2 * 16 * mbt * 4;
+#define OC_GS(B_, MB_)                                                                      \
+  if (bits == B_ && mbt == MB_) {                                                           \
+    hipLaunchKernelGGL((k_gemm_stream<B_, MB_, BF16>), grid, block, lds, st, a);            \
+    OC_HIP(hipGetLastError());                                                              \
+    return 0;                                                                               \
+  }
+  OC_GS(2, 1) OC_GS(2, 2) OC_GS(3, 1) OC_GS(3, 2) OC_GS(4, 1) OC_GS(4, 2) OC_GS(8, 1) OC_GS(8, 2)
+#undef OC_GS
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no streaming gemm for bits=%d M=%d", bits, M);
+}
+
 // Units in flight per wave of k_gemv_stream for this layer, or 0 when the
-// layer takes k_gemv: the streaming kernel serves wide layers (at least 1024
-// n-tiles) at M <= 8 whose x fits in 64 KB of LDS and whose groups are
-// powers of two >= 128.  OC_GEMV_STREAM=0 turns it off, =1 forces it where it
+// layer takes another path: the streaming kernel serves wide layers (at least
+// 1024 n-tiles) at M <= 4 (measured slower than k_gemv at M = 8) whose x (and
+// its k-block sums) fits in 80 KB of LDS and whose groups are powers of two
+// >= 128.  OC_GEMV_STREAM=0 turns it off, =1 forces it (up to M = 8) where it
 // applies; OC_GEMV_STREAM_D picks the depth (2 or 4).
 int stream_depth(const oc::Layout& L, int M, int gs) {
   const int e = env_int("OC_GEMV_STREAM", -1);
-  if (e == 0 || M > 8 || gs < 128 || log2_exact(gs) < 0) return 0;
+  if (e == 0 || M > (e == 1 ? 8 : 4) || gs < 128 || log2_exact(gs) < 0) return 0;
   if (stream_lds(L, M) > kStreamLds) return 0;
   if (e != 1 && L.NT < 1024) return 0;
   const int de = env_int("OC_GEMV_STREAM_D", 0);
@@ -785,6 +959,8 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
   const oc::Layout L = oc::make_layout(bits, K, N);
   size_t ws = 0;
   if (has_perm) ws += align256((size_t)M * K * 2);
+  const int gs = oc::eff_group(group_size, K);
+  if ((M <= kGemvMaxM && stream_depth(L, M, gs) > 0) || use_gemm_stream(L, M, gs)) return ws;
   if (M <= kGemvMaxM) {
     const GemvPlan p = plan_gemv(L, M, oc::eff_group(group_size, K));
     if (p.S > 1) ws += align256((size_t)p.S * M * L.N_pad * 4);
@@ -829,8 +1005,28 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     ws += align256((size_t)M * K * 2);
   }
   const bool bf16 = act_dtype == OC_DTYPE_BF16;
+  const int sd = M <= kGemvMaxM ? stream_depth(L, M, gs) : 0;
+  if (sd == 0 && use_gemm_stream(L, M, gs)) {
+    StreamArgs a;
+    a.x = xa;
+    a.w = (const uint8_t*)packed;
+    a.meta = meta;
+    a.bias = (const uint16_t*)bias;
+    a.y = (uint16_t*)y;
+    a.M = M;
+    a.K = K;
+    a.K_pad = L.K_pad;
+    a.N = N;
+    a.N_pad = L.N_pad;
+    a.NT_total = L.NT;
+    a.NU = L.NU;
+    a.G = G;
+    a.gs = gs;
+    a.gkb_shift = log2_exact(gs) - 7;
+    a.ldy = ldy;
+    return bf16 ? dispatch_gemm_stream<true>(bits, M, L, a, st) : dispatch_gemm_stream<false>(bits, M, L, a, st);
+  }
   if (M <= kGemvMaxM) {
-    const int sd = stream_depth(L, M, gs);
     if (sd > 0) {
       StreamArgs a;
       a.x = xa;

@@ -270,3 +270,28 @@ def test_gemm_streaming_variants(dev, bits, case, monkeypatch):
     else:  # forced on a narrow layer: fewer n-tiles than one workgroup's 4 waves in the last group
         monkeypatch.setenv("OC_GEMV_STREAM", "1")
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=95 + bits), 5, "fp16", bias=True)
+
+
+# Wide layers at mid M take the streaming GEMM (k-block x staging ring, MB row blocks per B
+# operand); K = 14336 at M = 4 takes it too (x does not fit the GEMV stream's LDS).
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [9, 16, 17, 32])
+def test_gemm_streaming_mid_m(dev, bits, m):
+    n = 16384 + 48 if bits != 3 else 16384 + 32
+    _gemm_check(dev, _case(1024, n, bits, seed=120 + bits + m), m, "fp16", bias=(m == 17))
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("case", ["act", "bf16", "g256", "long_k_m4", "narrow_forced"])
+def test_gemm_streaming_mid_m_variants(dev, bits, case, monkeypatch):
+    if case == "act":
+        _gemm_check(dev, _case(1024, 16384, bits, 128, True, seed=130 + bits), 20, "fp16", bias=True)
+    elif case == "bf16":
+        _gemm_check(dev, _case(1024, 16384, bits, seed=140 + bits), 24, "bf16", bias=True)
+    elif case == "g256":
+        _gemm_check(dev, _case(1024, 16384, bits, 256, False, seed=150 + bits), 12, "fp16")
+    elif case == "long_k_m4":
+        _gemm_check(dev, _case(14336, 16384, bits, seed=155 + bits), 4, "fp16")
+    else:
+        monkeypatch.setenv("OC_GEMM_STREAM", "1")
+        _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=160 + bits), 30, "fp16", bias=True)
