@@ -138,6 +138,32 @@ int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_part* parts,
                          int act_dtype, void* y, int ldy, void* workspace, size_t ws_bytes,
                          void* stream);
 
+/* ---------------------------------------------------------------- MoE experts -------------- */
+
+/* Workspace bytes oc_moe_gptq_forward needs (host only). */
+size_t oc_moe_workspace_bytes(int M, int H, int I, int topk);
+
+/* Mixture-of-experts block with GPTQ experts (all experts share bits and group size, no
+ * act-order).  For token t < M and slot j < topk, pair p = t * topk + j runs expert e = ids[p]
+ * (int32; ids outside [0, E) contribute nothing):
+ *   gate|up = x[t] @ W13_e^T (+ b13_e),  h = act(gate, up),  y[t] += weights[p] * (h @ W2_e^T + b2_e)
+ * act: 0 = SiLU(gate) * up, 1 = GELU-tanh(gate) * up, 2 = the gpt-oss combine
+ * (up.clamp(-limit, limit) + 1) * g * sigmoid(alpha * g) with g = gate.clamp(max=limit); each
+ * step is rounded to act_dtype as the reference's torch ops round.  weights are fp32 [M * topk].
+ * w13: E experts' oc_gptq_prepare output for the merged gate|up layer (H -> 2I, gate columns
+ * first), w13_stride bytes apart; meta13 their scale/zero words, meta13_stride words apart; b13
+ * [E, 2I] or NULL.  w2 / meta2 / b2 likewise for down (I -> H).  x [M, H], y [M, H] in act_dtype.
+ * Four launches on `stream`, no host synchronisation, no allocation.
+ * Replaces _UnfusedExperts.forward, onecomp/utils/unfuse_moe.py:61-114 (with the gpt-oss combine
+ * of :380-387) over GPTQ experts, and the WNA16 fused-experts dispatch of
+ * vllm_plugins/gptq/vllm_plugin.py:240-283. */
+int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, int topk, const int32_t* ids,
+                        const float* weights, const void* w13, size_t w13_stride, const uint32_t* meta13,
+                        size_t meta13_stride, const void* b13, const void* w2, size_t w2_stride,
+                        const uint32_t* meta2, size_t meta2_stride, const void* b2, int bits,
+                        int group_size, int act, float alpha, float limit, int act_dtype, void* y,
+                        void* workspace, size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------- DBF / MDBF ---------------- */
 
 /* Sizes of the internal sign layout of an R x Kd +-1 factor (host only): packed bytes, padded

@@ -35,6 +35,10 @@ SIGNATURES = {
                              c_size_t, P]),
     "oc_gptq_grouped_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
     "oc_gptq_gemm_grouped": (c_int, [P, c_int, c_int, P, c_int, c_int, P, c_int, P, c_size_t, P]),
+    "oc_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "oc_moe_gptq_forward": (c_int, [P, c_int, c_int, c_int, c_int, c_int, P, P, P, c_size_t, P, c_size_t,
+                                    P, P, c_size_t, P, c_size_t, P, c_int, c_int, c_int, ctypes.c_float,
+                                    ctypes.c_float, c_int, P, P, c_size_t, P]),
     "oc_dbf_layout": (c_int, [c_int, c_int, c_size_t_p, c_int_p, c_int_p]),
     "oc_dbf_unpack_signs": (c_int, [P, c_int, c_int, P, P]),
     "oc_dbf_prepare": (c_int, [P, c_int, c_int, P, P]),

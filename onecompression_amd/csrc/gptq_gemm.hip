@@ -169,6 +169,7 @@ struct GemvArgs {
   int M, K, N, N_pad, NT_total, NU, G, gs, gshift, S, ups;
   int ldy;   // row stride of y (N, or the fused width for a part of a fused layer)
   int bits;  // the part's bit width (grouped launches pick the decoder by it)
+  int out_f32;  // 1: write the fp32 sums (no bias) to partial[m * N_pad + n] instead of y
 };
 
 // One workgroup's share of a GEMV launch: block = column group * S + split.
@@ -306,7 +307,7 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
     const int m = 4 * (ln >> 4) + r;
     const int n = (ntg * NT + j) * 16 + (ln & 15);
     if (m >= a.M || ntg * NT + j >= a.NT_total) continue;
-    if (a.S == 1) {
+    if (a.S == 1 && !a.out_f32) {
       if (n < a.N) {
         float o = v;
         if (a.bias) o += BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
@@ -316,6 +317,41 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
       part[(size_t)m * a.N_pad + n] = v;
     }
   }
+}
+
+// MoE experts (moe.hip): one (token, expert) pair per group of workgroups,
+// the expert's weights found by its id on the device.
+struct MoeGemvArgs {
+  GemvArgs base;          // shape, bits, groups; x / w / meta / bias / y filled per pair
+  const int32_t* ids;     // [pairs] expert of each pair
+  int pairs, topk, E;
+  int x_per_pair;         // 1: x row = pair (down), 0: x row = pair / topk (gate|up)
+  size_t w_stride, meta_stride;  // bytes / words between experts
+  int bias_stride;        // elements between experts' bias vectors
+  int y_stride;           // elements between pairs' outputs (y or partial rows)
+  int ngroups;            // workgroups per pair
+};
+
+// units in flight for the MoE GEMV (M = 1, one n-tile per workgroup); 3-bit
+// layers with groups below 128 keep one unit (their register budget)
+template <int BITS, int CS>
+struct MoeDepth {
+  static constexpr int D = (CS == 1 && BITS == 3) ? 1 : ((BITS == 3 || BITS == 8) ? 2 : 4);
+};
+
+template <int BITS, int CS, int D, int W, bool BF16>
+__global__ __launch_bounds__(64 * W) void k_moe_gemv(const MoeGemvArgs g) {
+  const int p = blockIdx.x / g.ngroups, b = blockIdx.x % g.ngroups;
+  const int e = __builtin_amdgcn_readfirstlane(g.ids[p]);
+  if (e < 0 || e >= g.E) return;  // an invalid id contributes nothing (its rows stay unwritten)
+  GemvArgs a = g.base;
+  a.x = g.base.x + (size_t)(g.x_per_pair ? p : p / g.topk) * a.K;
+  a.w = g.base.w + (size_t)e * g.w_stride;
+  a.meta = g.base.meta + (size_t)e * g.meta_stride;
+  a.bias = g.base.bias ? g.base.bias + (size_t)e * g.bias_stride : nullptr;
+  a.y = g.base.y ? g.base.y + (size_t)p * g.y_stride : nullptr;
+  a.partial = g.base.partial ? g.base.partial + (size_t)p * g.y_stride : nullptr;
+  gemv_tile<BITS, 1, CS, D, W, 1, BF16>(a, b);
 }
 
 template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16>
@@ -1068,6 +1104,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     a.ups = p.ups;
     a.ldy = ldy;
     a.bits = bits;
+    a.out_f32 = 0;
     const int rc = bf16 ? dispatch_gemv_bits<true>(bits, p, a, st) : dispatch_gemv_bits<false>(bits, p, a, st);
     if (rc || p.S == 1) return rc;
     return launch_reduce(bf16, a.partial, p.S, M, N, L.N_pad, bias, y, ldy, st);
@@ -1334,10 +1371,239 @@ extern "C" int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_p
     a.ups = L.NU;
     a.ldy = ldy;
     a.bits = P.bits;
+    a.out_f32 = 0;
     ga.block_start[i] = blocks;
     blocks += L.NT;
   }
   for (int i = n_parts; i <= kMaxParts; ++i) ga.block_start[i] = blocks;
   ga.n_parts = n_parts;
   return bf16 ? launch_group<true>(gp, ga, blocks, st) : launch_group<false>(gp, ga, blocks, st);
+}
+
+// ---------------------------------------------------------------------------
+// MoE experts with GPTQ weights (OneComp's unfused experts,
+// onecomp/utils/unfuse_moe.py:61-114): for every token t and slot j of its
+// top-k, pair p = t * topk + j runs expert e = ids[p]:
+//   h13[p]  = x[t] @ W13_e^T (+ b13_e)          (gate | up, one GEMV per pair)
+//   h[p]    = act(gate) * up  or  the gpt-oss combine of gate and up
+//   part[p] = h[p] @ W2_e^T                     (fp32)
+//   y[t]    = sum_j w[t, j] * (part[t * topk + j] + b2_e)
+// Four launches, no host synchronisation; pairs with an id outside [0, E)
+// contribute nothing.
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __forceinline__ float oc_round_act(float v, bool bf16) {
+  return bf16 ? oc_bf2f(oc_f2bf(v)) : oc_h2f(oc_f2h(v));
+}
+
+// act: 0 = SiLU(gate) * up, 1 = GELU(tanh)(gate) * up, 2 = gpt-oss combine (alpha, limit),
+// each step rounded to the activation dtype as the reference's torch ops round
+template <bool BF16>
+__global__ void k_moe_act(const uint16_t* __restrict__ h13, int I, int pairs, int act, float alpha, float limit,
+                          const int32_t* __restrict__ ids, int E, uint16_t* __restrict__ h) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int p = blockIdx.y;
+  if (i >= I || p >= pairs) return;
+  const int e = ids[p];
+  float out = 0.f;
+  if (e >= 0 && e < E) {
+    const uint16_t* r = h13 + (size_t)p * 2 * I;
+    const float g = BF16 ? oc_bf2f(r[i]) : oc_h2f(r[i]);
+    const float u = BF16 ? oc_bf2f(r[I + i]) : oc_h2f(r[I + i]);
+    if (act == 2) {
+      const float gc = oc_round_act(fminf(g, limit), BF16);
+      const float uc = oc_round_act(fminf(fmaxf(u, -limit), limit), BF16);
+      const float sg = oc_round_act(1.f / (1.f + expf(-oc_round_act(gc * alpha, BF16))), BF16);
+      const float glu = oc_round_act(gc * sg, BF16);
+      out = oc_round_act(oc_round_act(uc + 1.f, BF16) * glu, BF16);
+    } else {
+      float a;
+      if (act == 0) {
+        a = g / (1.f + expf(-g));
+      } else {
+        const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+        a = 0.5f * g * (1.f + tanhf(c * (g + 0.044715f * g * g * g)));
+      }
+      out = oc_round_act(oc_round_act(a, BF16) * u, BF16);
+    }
+  }
+  h[(size_t)p * I + i] = BF16 ? oc_f2bf(out) : oc_f2h(out);
+}
+
+template <bool BF16>
+__global__ void k_moe_combine(const float* __restrict__ part, int H, int H_pad, int topk, int M,
+                              const int32_t* __restrict__ ids, int E, const float* __restrict__ w,
+                              const uint16_t* __restrict__ b2, uint16_t* __restrict__ y) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (n >= H || t >= M) return;
+  float acc = 0.f;
+  for (int j = 0; j < topk; ++j) {
+    const int p = t * topk + j, e = ids[p];
+    if (e < 0 || e >= E) continue;
+    float v = part[(size_t)p * H_pad + n];
+    if (b2) v += BF16 ? oc_bf2f(b2[(size_t)e * H + n]) : oc_h2f(b2[(size_t)e * H + n]);
+    acc = fmaf(w[p], v, acc);
+  }
+  y[(size_t)t * H + n] = BF16 ? oc_f2bf(acc) : oc_f2h(acc);
+}
+
+struct MoePlan {
+  size_t h13_off, h_off, part_off, bytes;
+};
+
+MoePlan plan_moe(int M, int H, int I, int topk) {
+  MoePlan p;
+  const size_t pairs = (size_t)M * topk;
+  const int h_pad = (H + 15) / 16 * 16;
+  p.h13_off = 0;
+  p.h_off = align256(pairs * 2 * I * 2);
+  p.part_off = p.h_off + align256(pairs * I * 2);
+  p.bytes = p.part_off + align256(pairs * h_pad * 4);
+  return p;
+}
+
+template <bool BF16>
+int launch_moe_gemv(const MoeGemvArgs& g, int bits, const GemvPlan& p, hipStream_t st) {
+  const dim3 grid((unsigned)(g.pairs * g.ngroups)), block(64 * p.w);
+#define OC_MG(B_, CS_, W_)                                                                              \
+  if (bits == B_ && p.cs == CS_ && p.w == W_) {                                                         \
+    hipLaunchKernelGGL((k_moe_gemv<B_, CS_, MoeDepth<B_, CS_>::D, W_, BF16>), grid, block, p.lds, st, g);   \
+    OC_HIP(hipGetLastError());                                                                          \
+    return 0;                                                                                           \
+  }
+#define OC_MGB(B_) OC_MG(B_, 4, 16) OC_MG(B_, 4, 8) OC_MG(B_, 4, 4) OC_MG(B_, 1, 8) OC_MG(B_, 1, 4)
+  OC_MGB(2) OC_MGB(3) OC_MGB(4) OC_MGB(8)
+#undef OC_MGB
+#undef OC_MG
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no MoE gemv kernel for bits=%d cs=%d w=%d", bits, p.cs, p.w);
+}
+
+}  // namespace
+
+extern "C" size_t oc_moe_workspace_bytes(int M, int H, int I, int topk) {
+  if (M <= 0 || H <= 0 || I <= 0 || topk <= 0) return 0;
+  return plan_moe(M, H, I, topk).bytes;
+}
+
+extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, int topk, const int32_t* ids,
+                                   const float* weights, const void* w13, size_t w13_stride, const uint32_t* meta13,
+                                   size_t meta13_stride, const void* b13, const void* w2, size_t w2_stride,
+                                   const uint32_t* meta2, size_t meta2_stride, const void* b2, int bits,
+                                   int group_size, int act, float alpha, float limit, int act_dtype, void* y,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  OC_REQUIRE(x && ids && weights && w13 && meta13 && w2 && meta2 && y, OC_ERR_INVALID, "null pointer");
+  OC_REQUIRE(bits == 2 || bits == 3 || bits == 4 || bits == 8, OC_ERR_UNSUPPORTED, "unsupported bits=%d", bits);
+  OC_REQUIRE(M >= 0 && H > 0 && I > 0 && E > 0 && topk > 0 && topk <= 64, OC_ERR_INVALID,
+             "bad shape M=%d H=%d I=%d E=%d topk=%d", M, H, I, E, topk);
+  OC_REQUIRE(H % 32 == 0 && I % 32 == 0, OC_ERR_SHAPE, "H=%d and I=%d must be multiples of 32", H, I);
+  OC_REQUIRE(act >= 0 && act <= 2, OC_ERR_UNSUPPORTED, "unknown activation %d", act);
+  OC_REQUIRE(act_dtype == OC_DTYPE_F16 || act_dtype == OC_DTYPE_BF16, OC_ERR_UNSUPPORTED, "bad act_dtype %d",
+             act_dtype);
+  if (M == 0) return 0;
+  const MoePlan mp = plan_moe(M, H, I, topk);
+  OC_REQUIRE(ws_bytes >= mp.bytes && workspace, OC_ERR_WORKSPACE,
+             "workspace of %zu bytes is smaller than the %zu required", ws_bytes, mp.bytes);
+  const oc::Layout L13 = oc::make_layout(bits, H, 2 * I), L2 = oc::make_layout(bits, I, H);
+  OC_REQUIRE(w13_stride >= oc::layout_bytes(L13) && w2_stride >= oc::layout_bytes(L2), OC_ERR_INVALID,
+             "expert strides smaller than one expert's packed weights");
+  const int gs13 = oc::eff_group(group_size, H), gs2 = oc::eff_group(group_size, I);
+  OC_REQUIRE(gs13 % 32 == 0 && gs2 % 32 == 0, OC_ERR_UNSUPPORTED, "group_size=%d", group_size);
+  const int G13 = (H + gs13 - 1) / gs13, G2 = (I + gs2 - 1) / gs2;
+  OC_REQUIRE(meta13_stride >= (size_t)G13 * L13.N_pad && meta2_stride >= (size_t)G2 * L2.N_pad, OC_ERR_INVALID,
+             "expert scale/zero strides too small");
+  hipStream_t st = (hipStream_t)stream;
+  const bool bf16 = act_dtype == OC_DTYPE_BF16;
+  uint8_t* ws = (uint8_t*)workspace;
+  uint16_t* h13 = (uint16_t*)(ws + mp.h13_off);
+  uint16_t* h = (uint16_t*)(ws + mp.h_off);
+  float* part = (float*)(ws + mp.part_off);
+  const int pairs = M * topk;
+  auto fill = [&](GemvArgs& a, const oc::Layout& L, int K, int N, int gs, int G) {
+    a = GemvArgs{};
+    a.M = 1;
+    a.K = K;
+    a.N = N;
+    a.N_pad = L.N_pad;
+    a.NT_total = L.NT;
+    a.NU = L.NU;
+    a.G = G;
+    a.gs = gs;
+    a.gshift = log2_exact(gs);
+    a.S = 1;
+    a.ups = L.NU;
+    a.bits = bits;
+  };
+  // 1. gate | up for every pair
+  {
+    const GemvPlan p = plan_gemv(L13, 1, gs13);
+    MoeGemvArgs g = {};
+    fill(g.base, L13, H, 2 * I, gs13, G13);
+    g.base.x = (const uint16_t*)x;
+    g.base.w = (const uint8_t*)w13;
+    g.base.meta = meta13;
+    g.base.bias = (const uint16_t*)b13;
+    g.base.y = h13;
+    g.base.ldy = 2 * I;
+    g.ids = ids;
+    g.pairs = pairs;
+    g.topk = topk;
+    g.E = E;
+    g.x_per_pair = 0;
+    g.w_stride = w13_stride;
+    g.meta_stride = meta13_stride;
+    g.bias_stride = 2 * I;
+    g.y_stride = 2 * I;
+    g.ngroups = L13.NT;
+    GemvPlan q = p;
+    q.nt = 1;
+    const int rc = bf16 ? launch_moe_gemv<true>(g, bits, q, st) : launch_moe_gemv<false>(g, bits, q, st);
+    if (rc) return rc;
+  }
+  // 2. activation
+  {
+    const dim3 grid((I + 255) / 256, pairs);
+    if (bf16) hipLaunchKernelGGL(k_moe_act<true>, grid, dim3(256), 0, st, h13, I, pairs, act, alpha, limit, ids, E, h);
+    else hipLaunchKernelGGL(k_moe_act<false>, grid, dim3(256), 0, st, h13, I, pairs, act, alpha, limit, ids, E, h);
+    OC_HIP(hipGetLastError());
+  }
+  // 3. down for every pair, fp32
+  {
+    const GemvPlan p = plan_gemv(L2, 1, gs2);
+    MoeGemvArgs g = {};
+    fill(g.base, L2, I, H, gs2, G2);
+    g.base.x = h;
+    g.base.w = (const uint8_t*)w2;
+    g.base.meta = meta2;
+    g.base.partial = part;
+    g.base.out_f32 = 1;
+    g.base.ldy = H;
+    g.ids = ids;
+    g.pairs = pairs;
+    g.topk = topk;
+    g.E = E;
+    g.x_per_pair = 1;
+    g.w_stride = w2_stride;
+    g.meta_stride = meta2_stride;
+    g.bias_stride = 0;
+    g.y_stride = L2.N_pad;
+    g.ngroups = L2.NT;
+    GemvPlan q = p;
+    q.nt = 1;
+    const int rc = bf16 ? launch_moe_gemv<true>(g, bits, q, st) : launch_moe_gemv<false>(g, bits, q, st);
+    if (rc) return rc;
+  }
+  // 4. weighted sum over the top-k (+ down bias)
+  {
+    const dim3 grid((H + 255) / 256, M);
+    if (bf16)
+      hipLaunchKernelGGL(k_moe_combine<true>, grid, dim3(256), 0, st, part, H, L2.N_pad, topk, M, ids, E, weights,
+                         (const uint16_t*)b2, (uint16_t*)y);
+    else
+      hipLaunchKernelGGL(k_moe_combine<false>, grid, dim3(256), 0, st, part, H, L2.N_pad, topk, M, ids, E, weights,
+                         (const uint16_t*)b2, (uint16_t*)y);
+    OC_HIP(hipGetLastError());
+  }
+  return 0;
 }

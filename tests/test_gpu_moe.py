@@ -1,0 +1,121 @@
+"""GPU parity of the MoE block over GPTQ experts (oc_moe_gptq_forward) against the oracle's
+restatement of _UnfusedExperts.forward (onecomp/utils/unfuse_moe.py:61-114)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq as og
+from oracle import moe as om
+from onecompression_amd import hf, moe, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _w32(c, dtype):
+    g = og.default_g_idx(c.in_features, c.group_size)
+    w = og.dequantize(_np(c.qweight), _np(c.qzeros), _np(c.scales), g, c.bits, "gptq", dtype)
+    return og.to_f32(w, dtype)
+
+
+def _build(E, H, I, bits, gs, bias, dtype, seed):
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    cases, ref = [], []
+    gen = torch.Generator().manual_seed(seed)
+
+    def case(k, n, s):
+        # weights of about the same magnitude at every bit width, so that the two chained
+        # products stay far inside the fp16 range (8-bit codes span 256 levels)
+        c = synth.gptq_case("w", k, n, bits, gs, False, seed=s)
+        c.scales = (c.scales.float() * (4.0 / (1 << bits))).to(torch.float16)
+        return c
+
+    for e in range(E):
+        g = case(H, I, seed + 3 * e)
+        u = case(H, I, seed + 3 * e + 1)
+        d = case(I, H, seed + 3 * e + 2)
+        ex = {"gate": _w32(g, dtype), "up": _w32(u, dtype), "down": _w32(d, dtype)}
+        bs = None
+        if bias:
+            bs = [(torch.randn(n, generator=gen) * 0.05).to(td) for n in (I, I, H)]
+            ex.update(gate_bias=bs[0].float().numpy(), up_bias=bs[1].float().numpy(),
+                      down_bias=bs[2].float().numpy())
+        cases.append((g, u, d, bs))
+        ref.append(ex)
+    return cases, ref
+
+
+def _prepare(cases, bits, gs, dev):
+    dv = lambda c: (c.qweight.to(dev), c.qzeros.to(dev), c.scales.to(dev))  # noqa: E731
+    bias = cases[0][3] is not None
+    return moe.prepare_experts([dv(g) for g, _, _, _ in cases], [dv(u) for _, u, _, _ in cases],
+                               [dv(d) for _, _, d, _ in cases], bits, gs,
+                               gate_up_bias=[torch.cat([b[0], b[1]]).to(dev) for *_, b in cases] if bias else None,
+                               down_bias=[b[2].to(dev) for *_, b in cases] if bias else None)
+
+
+def _routing(M, k, E, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(M)]).to(torch.int32)
+    w = torch.softmax(torch.randn(M, k, generator=g), dim=-1)
+    return idx, w
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("act", ["silu", "gelu_pytorch_tanh", "gpt_oss"])
+@pytest.mark.parametrize("m", [1, 5])
+def test_moe_matches_oracle(dev, bits, act, m):
+    E, H, I, k, gs = 6, 256, 128, 2, 128
+    cases, ref = _build(E, H, I, bits, gs, act == "gpt_oss", "fp16", seed=10 * bits + m)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=m)
+    idx, w = _routing(m, k, E, seed=m + bits)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, act).float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref,
+                          "gelu_tanh" if act == "gelu_pytorch_tanh" else act)
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
+
+
+def test_moe_bf16_group32_topk4_and_invalid_slot(dev):
+    E, H, I, k, gs, m = 8, 256, 96, 4, 32, 3
+    cases, ref = _build(E, H, I, 4, gs, True, "bf16", seed=7)
+    ex = _prepare(cases, 4, gs, dev)
+    x = synth.activations(m, H, torch.bfloat16, seed=2)
+    idx, w = _routing(m, k, E, seed=5)
+    idx[1, 2] = -1  # a slot the router left empty contributes nothing
+    idx[2, 0] = E
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "gpt_oss").float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss", dtype="bf16")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 2e-2, err
+
+
+def test_gptq_experts_module_forward(dev):
+    """The HF-path drop-in over hf.GPTQLinear experts, both router argument conventions."""
+    E, H, I, k, gs, bits, m = 4, 256, 64, 2, 128, 4, 4
+    cases, ref = _build(E, H, I, bits, gs, False, "fp16", seed=21)
+
+    def lin(c):
+        sd = {"qweight": c.qweight, "scales": c.scales, "qzeros": c.qzeros}
+        return hf.GPTQLinear.from_saved_state(sd, c.in_features, c.out_features, bits, gs,
+                                              checkpoint_format="gptq")
+
+    experts = []
+    for g, u, d, _ in cases:
+        e = torch.nn.Module()
+        e.gate_proj, e.up_proj, e.down_proj = lin(g), lin(u), lin(d)
+        experts.append(e)
+    block = moe.GPTQExperts(E, experts, act="silu").to(dev)
+    x = synth.activations(m, H, torch.float16, seed=4)
+    idx, w = _routing(m, k, E, seed=8)
+    y1 = block(x.to(dev), top_k_index=idx.to(dev), top_k_weights=w.to(dev))
+    y2 = block(x.to(dev), router_indices=idx.to(dev), routing_weights=w.to(dev))
+    assert torch.equal(y1, y2)
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
+    err = float(np.max(np.abs(y1.float().cpu().numpy() - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
