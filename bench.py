@@ -177,6 +177,59 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
 
 RIDGE_FLOP_PER_BYTE = MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
+# MoE blocks with GPTQ experts (not a BASELINE config): name, hidden, intermediate, experts, top-k, Ms
+MOE_SHAPES = [("Qwen3-30B-A3B experts", 2048, 768, 128, 8, (1, 8)),
+              ("Mixtral-8x7B experts", 4096, 14336, 8, 2, (1, 4))]
+
+
+def report_moe(dev, bits=4, gs=128, routings=16):
+    """µs per MoE block forward (oc_moe_gptq_forward: gate|up, act, down, combine) at decode M.
+
+    Bytes: `GBps` counts each expert the routing hit once (its packed weights + fp16 scales +
+    packed zeros, as a checkpoint stores them) plus x and y; `pair_GBps` counts one expert read
+    per (token, slot) pair, which is what the kernels read (an expert hit by two tokens is read
+    twice).  The routing cycles over `routings` seeded draws and the expert buffers over >= 1 GiB
+    of copies, so the Infinity Cache cannot serve the weights."""
+    import torch
+
+    from onecompression_amd import moe, synth
+
+    out = []
+    for name, H, I, E, k, ms in MOE_SHAPES:
+        g13, g2 = H // gs, I // gs
+        e_bytes = (H * 2 * I * bits // 8 + g13 * 2 * I * (2 * 8 + bits) // 8
+                   + I * H * bits // 8 + g2 * H * (2 * 8 + bits) // 8)
+        trios = []
+        for j in range(2):
+            cs = [synth.gptq_case(n_, a, b, bits, gs, False, seed=900 + 3 * j + t).to(dev)
+                  for t, (n_, a, b) in enumerate((("gate", H, I), ("up", H, I), ("down", I, H)))]
+            trios.append([(c.qweight, c.qzeros, c.scales) for c in cs])
+        copies = max(1, min(8, -(-(1 << 30) // (E * e_bytes))))
+        exs = [moe.prepare_experts([trios[e % 2][0] for e in range(E)], [trios[e % 2][1] for e in range(E)],
+                                   [trios[e % 2][2] for e in range(E)], bits, gs) for _ in range(copies)]
+        del trios
+        gen = torch.Generator().manual_seed(77)
+        for m in ms:
+            x = synth.activations(m, H, torch.float16, seed=600 + m).to(dev)
+            rts = []
+            for _ in range(routings):
+                idx = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(m)]).to(torch.int32)
+                w = torch.softmax(torch.randn(m, k, generator=gen), dim=-1)
+                rts.append((idx.to(dev), w.to(dev), len(set(idx.flatten().tolist()))))
+            n_rot = routings * copies
+            us = _time_graph(lambda i: moe.moe_forward(x, rts[i % routings][0], rts[i % routings][1],
+                                                       exs[(i // routings) % copies]), n_rot, 2 * n_rot)
+            distinct = sum(r[2] for r in rts) / routings
+            io = 4 * m * H
+            out.append({"block": name, "H": H, "I": I, "E": E, "topk": k, "bits": bits, "gs": gs, "M": m,
+                        "dtype": "fp16", "us": round(us, 2), "experts_hit": round(distinct, 2),
+                        "GBps": round((distinct * e_bytes + io) / (us * 1e-6) / 1e9, 1),
+                        "pair_GBps": round((m * k * e_bytes + io) / (us * 1e-6) / 1e9, 1),
+                        "frac_hbm_peak": round((distinct * e_bytes + io) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del exs
+        torch.cuda.empty_cache()
+    return out
+
 
 def _time_graph(launch, copies, iters, warm=2):
     """Mean µs per launch of `iters` launches (launch(i) uses copy i % copies) in one HIP graph."""
@@ -408,6 +461,9 @@ def main():
                     help="comma-separated BASELINE configs: print only their per-config report")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the M=2048 dequant-GEMM measurement (config 4 gate_up, bf16)")
+    ap.add_argument("--moe-only", action="store_true",
+                    help="only the MoE block report (GPTQ experts at decode M)")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE block report")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -433,6 +489,9 @@ def main():
         return
     if args.gemm_only:
         print(json.dumps(bench_gemm_large(2048, args.steps, args.warmup, dev)))
+        return
+    if args.moe_only:
+        print(json.dumps({"moe": report_moe(dev)}))
         return
     r = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev)
     dom = max(r["kernels"], key=lambda k: k["us"])
@@ -479,6 +538,11 @@ def main():
             out["configs"] = report_configs(dev)
         except Exception as e:  # reported, never hides the main line
             out["configs"] = {"error": str(e)}
+    if not args.no_moe:
+        try:
+            out["moe"] = report_moe(dev)
+        except Exception as e:  # reported, never hides the main line
+            out["moe"] = {"error": str(e)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(r["cases"], args.m)
         c0 = synth_config0()

@@ -172,9 +172,14 @@ struct GemvArgs {
   int out_f32;  // 1: write the fp32 sums (no bias) to partial[m * N_pad + n] instead of y
 };
 
-// One workgroup's share of a GEMV launch: block = column group * S + split.
-template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16>
-__device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
+// The accumulation of one workgroup of a GEMV: each wave streams units
+// u0 + wave, u0 + wave + W, ... (< u1) of the n-tiles nt[] and sums its share
+// of x @ W^T into yacc (lane l: column l % 16 of n-tile j, rows 4 (l / 16) + r).
+// rows <= a.M x rows are live; xrow(q, m) is the start of row m, which this
+// lane's x chunk q (of XCH) belongs to.  The wave's LDS x slot holds a.M rows.
+template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16, class XRow>
+__device__ __forceinline__ void gemv_accum(const GemvArgs& a, const int (&nt)[NT], const int u0, const int u1,
+                                           const int rows, XRow xrow, oc_f4 (&yacc)[NT]) {
   using GG = Geo<BITS>;
   constexpr int U = GG::U, P = GG::P;
   constexpr int SPK = 4 / CS;        // correction segments per k-block
@@ -183,21 +188,15 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
   constexpr float OFF = dec_offset<BITS, BF16>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ntg = block / a.S, s = block % a.S;
   const int col = lane & 15, kq = lane >> 4;
   const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<BF16>());
   const uint32_t one16 = BF16 ? 0x3F803F80u : 0x3C003C00u;
   const oc_u4 ones = oc_u4{one16, one16, one16, one16};
 
-  int nt[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) nt[j] = min(ntg * NT + j, a.NT_total - 1);
-
-  const int u0 = s * a.ups, u1 = min(u0 + a.ups, a.NU);
   const int n_my = u0 + wave < u1 ? (u1 - u0 - wave + W - 1) / W : 0;
 
   // x chunk c of a unit (16 B = 8 k): row c / (16U), k offset 8 * (c % (16U))
-  auto xchunk_ok = [&](int c) { return c < a.M * 16 * U; };
+  auto xchunk_ok = [&](int c) { return c < rows * 16 * U; };
 
   uint32_t buf[D][NT][4 * P];
   uint32_t mbuf[D][NT][MPU];
@@ -207,7 +206,7 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
     for (int q = 0; q < XCH; ++q) {
       const int c = lane + 64 * q;
       const int m = c / (16 * U), k = unit * U * 128 + 8 * (c % (16 * U));
-      xb[q] = (xchunk_ok(c) && k < a.K) ? *(const oc_u4*)(a.x + (size_t)m * a.K + k) : oc_u4{0u, 0u, 0u, 0u};
+      xb[q] = (xchunk_ok(c) && k < a.K) ? *(const oc_u4*)(xrow(q, m) + k) : oc_u4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -234,9 +233,8 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
 
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* xslot = (uint16_t*)smem + (size_t)wave * a.M * XW;  // this wave's x rows
-  const uint16_t* arow = xslot + min(col, a.M - 1) * XW + 8 * kq;
+  const uint16_t* arow = xslot + min(col, rows - 1) * XW + 8 * kq;
 
-  oc_f4 yacc[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) yacc[j] = oc_f4{0.f, 0.f, 0.f, 0.f};
 
@@ -288,8 +286,24 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
       if (i + D < n_my) load_unit(u + W * D, buf[d], mbuf[d], xbuf[d]);
     }
   }
+}
+
+// One workgroup's share of a GEMV launch: block = column group * S + split.
+template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16>
+__device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ntg = block / a.S, s = block % a.S;
+  int nt[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) nt[j] = min(ntg * NT + j, a.NT_total - 1);
+  const int u0 = s * a.ups, u1 = min(u0 + a.ups, a.NU);
+  oc_f4 yacc[NT];
+  gemv_accum<BITS, NT, CS, D, W, XCH, BF16>(a, nt, u0, u1, a.M,
+                                            [&](int, int m) { return a.x + (size_t)m * a.K; }, yacc);
 
   // ---- reduce the W waves ----
+  extern __shared__ __align__(16) uint8_t smem[];
   __syncthreads();  // x slots no longer needed: reuse LDS
   float* red = (float*)smem;  // [W][NT][4][64]
 #pragma unroll
@@ -319,39 +333,219 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
   }
 }
 
-// MoE experts (moe.hip): one (token, expert) pair per group of workgroups,
-// the expert's weights found by its id on the device.
-struct MoeGemvArgs {
-  GemvArgs base;          // shape, bits, groups; x / w / meta / bias / y filled per pair
-  const int32_t* ids;     // [pairs] expert of each pair
+// ---------------------------------------------------------------------------
+// MoE experts at decode sizes.  Pair p = t * topk + j (token t, top-k slot j)
+// runs expert ids[p].  The pairs that share an expert are served RM at a
+// time: the pairs of expert e, in pair order, are cut into runs of RM, and the
+// workgroups of the first pair of each run read e's weights once for all the
+// run's rows (the rows of the MFMA A operand); the other pairs' workgroups
+// exit.  With RM = 1 every pair is its own run.  RM > 1 needs pairs <= 64
+// (one id per lane of a wave).
+// ---------------------------------------------------------------------------
+struct MoeArgs {
+  GemvArgs base;        // the layer's shape; M = RM (x slot rows); w / meta = expert 0
+  const int32_t* ids;   // [pairs]
+  const uint16_t* bias; // gate|up bias [E, 2I], or null
+  uint16_t* out;        // gate|up launch: h [pairs, I]
+  float* part;          // down launch: fp32 sums per pair [pairs, N_pad]
   int pairs, topk, E;
-  int x_per_pair;         // 1: x row = pair (down), 0: x row = pair / topk (gate|up)
+  int ntiles;           // workgroups per pair: I / 16 (gate|up) or NT(H) (down)
+  int I;                // intermediate size
+  int act;
+  float alpha, limit;
   size_t w_stride, meta_stride;  // bytes / words between experts
-  int bias_stride;        // elements between experts' bias vectors
-  int y_stride;           // elements between pairs' outputs (y or partial rows)
-  int ngroups;            // workgroups per pair
 };
 
-// units in flight for the MoE GEMV (M = 1, one n-tile per workgroup); 3-bit
-// layers with groups below 128 keep one unit (their register budget)
-template <int BITS, int CS>
-struct MoeDepth {
-  static constexpr int D = (CS == 1 && BITS == 3) ? 1 : ((BITS == 3 || BITS == 8) ? 2 : 4);
+struct MoeRun {
+  int e;          // expert of the workgroup's pair
+  int rows;       // rows this workgroup serves (0: none)
+  uint64_t mask;  // pairs of the run and of later runs of e (bit q = pair q), RM > 1 only
 };
 
-template <int BITS, int CS, int D, int W, bool BF16>
-__global__ __launch_bounds__(64 * W) void k_moe_gemv(const MoeGemvArgs g) {
-  const int p = blockIdx.x / g.ngroups, b = blockIdx.x % g.ngroups;
-  const int e = __builtin_amdgcn_readfirstlane(g.ids[p]);
-  if (e < 0 || e >= g.E) return;  // an invalid id contributes nothing (its rows stay unwritten)
+template <int RM>
+__device__ __forceinline__ MoeRun moe_run(const MoeArgs& g, const int p) {
+  MoeRun r;
+  r.e = __builtin_amdgcn_readfirstlane(g.ids[p]);
+  r.rows = 0;
+  r.mask = 0;
+  if (r.e < 0 || r.e >= g.E) return r;
+  if constexpr (RM == 1) {
+    r.rows = 1;
+  } else {
+    const int lane = threadIdx.x & 63;
+    const int id = lane < g.pairs ? g.ids[lane] : -1;
+    const uint64_t same = __ballot(id == r.e);
+    const uint64_t below = same & ((1ull << p) - 1ull);
+    if (__popcll(below) % RM) return r;  // a run of an earlier pair covers p
+    r.mask = same & ~below;
+    r.rows = min(RM, __popcll(r.mask));
+  }
+  return r;
+}
+
+// pair of row m (< rows) of a run
+template <int RM>
+__device__ __forceinline__ int moe_pair(const MoeRun& r, const int p, int m) {
+  if constexpr (RM == 1) {
+    return p;
+  } else {
+    uint64_t b = r.mask;
+    for (; m > 0; --m) b &= b - 1ull;
+    return (int)__builtin_ctzll(b);
+  }
+}
+
+// per-lane x row offsets (elements) of the lane's XCH chunks: row m = chunk / (16 U)
+template <int BITS, int XCH, int RM>
+__device__ __forceinline__ void moe_xrows(const MoeRun& r, const int p, const int div, const int K, const int rows,
+                                          int (&xo)[XCH]) {
+  constexpr int U = Geo<BITS>::U;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int q = 0; q < XCH; ++q) {
+    const int m = (lane + 64 * q) / (16 * U);
+    xo[q] = m < rows ? (moe_pair<RM>(r, p, m) / div) * K : 0;
+  }
+}
+
+__device__ __forceinline__ float oc_round_act(float v, bool bf16) {
+  return bf16 ? oc_bf2f(oc_f2bf(v)) : oc_h2f(oc_f2h(v));
+}
+
+// act: 0 = SiLU(gate) * up, 1 = GELU(tanh)(gate) * up, 2 = gpt-oss combine (alpha, limit),
+// each step rounded to the activation dtype as the reference's torch ops round
+template <bool BF16>
+__device__ __forceinline__ float moe_act(float g, float u, int act, float alpha, float limit) {
+  if (act == 2) {
+    const float gc = oc_round_act(fminf(g, limit), BF16);
+    const float uc = oc_round_act(fminf(fmaxf(u, -limit), limit), BF16);
+    const float sg = oc_round_act(1.f / (1.f + expf(-oc_round_act(gc * alpha, BF16))), BF16);
+    const float glu = oc_round_act(gc * sg, BF16);
+    return oc_round_act(oc_round_act(uc + 1.f, BF16) * glu, BF16);
+  }
+  float a;
+  if (act == 0) {
+    a = g / (1.f + expf(-g));
+  } else {
+    const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+    a = 0.5f * g * (1.f + tanhf(c * (g + 0.044715f * g * g * g)));
+  }
+  return oc_round_act(oc_round_act(a, BF16) * u, BF16);
+}
+
+// gate|up of the merged layer (H -> 2I: gate columns, then up columns) and the
+// activation: workgroup (p, j) computes gate tile j and up tile j (n-tiles j and
+// I/16 + j) for its run's rows and writes h[pair, 16 j .. 16 j + 15].
+template <int BITS, int CS, int D, int W, int XCH, int RM, bool BF16>
+__global__ __launch_bounds__(64 * W) void k_moe_gate_up(const MoeArgs g) {
+  const int p = blockIdx.x / g.ntiles, j = blockIdx.x % g.ntiles;
+  const MoeRun r = moe_run<RM>(g, p);
+  if (r.rows == 0) return;
   GemvArgs a = g.base;
-  a.x = g.base.x + (size_t)(g.x_per_pair ? p : p / g.topk) * a.K;
-  a.w = g.base.w + (size_t)e * g.w_stride;
-  a.meta = g.base.meta + (size_t)e * g.meta_stride;
-  a.bias = g.base.bias ? g.base.bias + (size_t)e * g.bias_stride : nullptr;
-  a.y = g.base.y ? g.base.y + (size_t)p * g.y_stride : nullptr;
-  a.partial = g.base.partial ? g.base.partial + (size_t)p * g.y_stride : nullptr;
-  gemv_tile<BITS, 1, CS, D, W, 1, BF16>(a, b);
+  a.w = g.base.w + (size_t)r.e * g.w_stride;
+  a.meta = g.base.meta + (size_t)r.e * g.meta_stride;
+  int xo[XCH];
+  moe_xrows<BITS, XCH, RM>(r, p, g.topk, a.K, r.rows, xo);
+  const int nt[2] = {j, g.ntiles + j};
+  oc_f4 yacc[2];
+  gemv_accum<BITS, 2, CS, D, W, XCH, BF16>(a, nt, 0, a.NU, r.rows, [&](int q, int) { return a.x + xo[q]; },
+                                           yacc);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  extern __shared__ __align__(16) uint8_t smem[];
+  __syncthreads();  // x slots no longer needed: reuse LDS
+  float* red = (float*)smem;  // [W][2][4][64]
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) red[((wave * 2 + t) * 4 + rr) * 64 + lane] = yacc[t][rr];
+  __syncthreads();
+  for (int el = threadIdx.x; el < 256; el += 64 * W) {
+    const int ln = el & 63, m = 4 * (ln >> 4) + (el >> 6);
+    if (m >= r.rows) continue;
+    float gv = 0.f, uv = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < W; ++ww) {
+      gv += red[(ww * 2) * 256 + el];
+      uv += red[(ww * 2 + 1) * 256 + el];
+    }
+    const int i = 16 * j + (ln & 15);
+    if (g.bias) {
+      const uint16_t* b = g.bias + (size_t)r.e * 2 * g.I;
+      gv += BF16 ? oc_bf2f(b[i]) : oc_h2f(b[i]);
+      uv += BF16 ? oc_bf2f(b[g.I + i]) : oc_h2f(b[g.I + i]);
+    }
+    const float h = moe_act<BF16>(oc_round_act(gv, BF16), oc_round_act(uv, BF16), g.act, g.alpha, g.limit);
+    g.out[(size_t)moe_pair<RM>(r, p, m) * g.I + i] = BF16 ? oc_f2bf(h) : oc_f2h(h);
+  }
+}
+
+// down (I -> H) per run: the fp32 sums of the run's rows go to part[pair].
+template <int BITS, int CS, int D, int W, int XCH, int RM, bool BF16>
+__global__ __launch_bounds__(64 * W) void k_moe_down(const MoeArgs g) {
+  const int p = blockIdx.x / g.ntiles, j = blockIdx.x % g.ntiles;
+  const int lane = threadIdx.x & 63;
+  const MoeRun r = moe_run<RM>(g, p);
+  if (r.rows == 0) return;
+  GemvArgs a = g.base;
+  a.w = g.base.w + (size_t)r.e * g.w_stride;
+  a.meta = g.base.meta + (size_t)r.e * g.meta_stride;
+  int xo[XCH];
+  moe_xrows<BITS, XCH, RM>(r, p, 1, a.K, r.rows, xo);
+  const int nt[1] = {j};
+  oc_f4 yacc[1];
+  gemv_accum<BITS, 1, CS, D, W, XCH, BF16>(a, nt, 0, a.NU, r.rows, [&](int q, int) { return a.x + xo[q]; },
+                                           yacc);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  extern __shared__ __align__(16) uint8_t smem[];
+  __syncthreads();
+  float* red = (float*)smem;  // [W][4][64]
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) red[(wave * 4 + rr) * 64 + lane] = yacc[0][rr];
+  __syncthreads();
+  for (int el = threadIdx.x; el < 256; el += 64 * W) {
+    const int ln = el & 63, m = 4 * (ln >> 4) + (el >> 6);
+    if (m >= r.rows) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < W; ++ww) v += red[ww * 256 + el];
+    g.part[(size_t)moe_pair<RM>(r, p, m) * a.N_pad + 16 * j + (ln & 15)] = v;
+  }
+}
+
+// y[t] = sum over t's valid slots, in slot order, of w[p] * (part[p] + b2_e); zero for a token
+// with no valid slot.  The ids, then the sums, weights and biases of 8 slots at a time are
+// loaded before any is used (two dependent round trips per 8 slots, not two per slot).
+template <bool BF16>
+__global__ void k_moe_combine(const float* __restrict__ part, int H, int H_pad, int topk, int M,
+                              const int32_t* __restrict__ ids, int E, const float* __restrict__ w,
+                              const uint16_t* __restrict__ b2, uint16_t* __restrict__ y) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (n >= H || t >= M) return;
+  float acc = 0.f;
+  for (int j0 = 0; j0 < topk; j0 += 8) {
+    int e[8], pp[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      pp[jj] = t * topk + min(j0 + jj, topk - 1);
+      e[jj] = ids[pp[jj]];
+    }
+    float v[8], wt[8], bv[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const bool ok = j0 + jj < topk && e[jj] >= 0 && e[jj] < E;
+      e[jj] = ok ? e[jj] : -1;
+      v[jj] = part[(size_t)pp[jj] * H_pad + n];
+      wt[jj] = w[pp[jj]];
+      const uint16_t bb = b2 ? b2[(size_t)(ok ? e[jj] : 0) * H + n] : (uint16_t)0;
+      bv[jj] = BF16 ? oc_bf2f(bb) : oc_h2f(bb);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      if (e[jj] >= 0) acc = fmaf(wt[jj], v[jj] + bv[jj], acc);
+  }
+  y[(size_t)t * H + n] = BF16 ? oc_f2bf(acc) : oc_f2h(acc);
 }
 
 template <int BITS, int NT, int CS, int D, int W, int XCH, bool BF16>
@@ -1384,107 +1578,100 @@ extern "C" int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_p
 // MoE experts with GPTQ weights (OneComp's unfused experts,
 // onecomp/utils/unfuse_moe.py:61-114): for every token t and slot j of its
 // top-k, pair p = t * topk + j runs expert e = ids[p]:
-//   h13[p]  = x[t] @ W13_e^T (+ b13_e)          (gate | up, one GEMV per pair)
-//   h[p]    = act(gate) * up  or  the gpt-oss combine of gate and up
-//   part[p] = h[p] @ W2_e^T                     (fp32)
-//   y[t]    = sum_j w[t, j] * (part[t * topk + j] + b2_e)
-// Four launches, no host synchronisation; pairs with an id outside [0, E)
+//   h[p]    = act(x[t] @ Wg_e^T (+ bg_e), x[t] @ Wu_e^T (+ bu_e))   (k_moe_gate_up)
+//   part[p] = h[p] @ W2_e^T                                         (k_moe_down, fp32)
+//   y[t]    = sum_j w[t, j] * (part[t * topk + j] + b2_e)           (k_moe_combine)
+// Three launches, no host synchronisation; pairs with an id outside [0, E)
 // contribute nothing.
 // ---------------------------------------------------------------------------
 namespace {
 
-__device__ __forceinline__ float oc_round_act(float v, bool bf16) {
-  return bf16 ? oc_bf2f(oc_f2bf(v)) : oc_h2f(oc_f2h(v));
-}
-
-// act: 0 = SiLU(gate) * up, 1 = GELU(tanh)(gate) * up, 2 = gpt-oss combine (alpha, limit),
-// each step rounded to the activation dtype as the reference's torch ops round
-template <bool BF16>
-__global__ void k_moe_act(const uint16_t* __restrict__ h13, int I, int pairs, int act, float alpha, float limit,
-                          const int32_t* __restrict__ ids, int E, uint16_t* __restrict__ h) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const int p = blockIdx.y;
-  if (i >= I || p >= pairs) return;
-  const int e = ids[p];
-  float out = 0.f;
-  if (e >= 0 && e < E) {
-    const uint16_t* r = h13 + (size_t)p * 2 * I;
-    const float g = BF16 ? oc_bf2f(r[i]) : oc_h2f(r[i]);
-    const float u = BF16 ? oc_bf2f(r[I + i]) : oc_h2f(r[I + i]);
-    if (act == 2) {
-      const float gc = oc_round_act(fminf(g, limit), BF16);
-      const float uc = oc_round_act(fminf(fmaxf(u, -limit), limit), BF16);
-      const float sg = oc_round_act(1.f / (1.f + expf(-oc_round_act(gc * alpha, BF16))), BF16);
-      const float glu = oc_round_act(gc * sg, BF16);
-      out = oc_round_act(oc_round_act(uc + 1.f, BF16) * glu, BF16);
-    } else {
-      float a;
-      if (act == 0) {
-        a = g / (1.f + expf(-g));
-      } else {
-        const float c = 0.7978845608028654f;  // sqrt(2 / pi)
-        a = 0.5f * g * (1.f + tanhf(c * (g + 0.044715f * g * g * g)));
-      }
-      out = oc_round_act(oc_round_act(a, BF16) * u, BF16);
-    }
-  }
-  h[(size_t)p * I + i] = BF16 ? oc_f2bf(out) : oc_f2h(out);
-}
-
-template <bool BF16>
-__global__ void k_moe_combine(const float* __restrict__ part, int H, int H_pad, int topk, int M,
-                              const int32_t* __restrict__ ids, int E, const float* __restrict__ w,
-                              const uint16_t* __restrict__ b2, uint16_t* __restrict__ y) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  const int t = blockIdx.y;
-  if (n >= H || t >= M) return;
-  float acc = 0.f;
-  for (int j = 0; j < topk; ++j) {
-    const int p = t * topk + j, e = ids[p];
-    if (e < 0 || e >= E) continue;
-    float v = part[(size_t)p * H_pad + n];
-    if (b2) v += BF16 ? oc_bf2f(b2[(size_t)e * H + n]) : oc_h2f(b2[(size_t)e * H + n]);
-    acc = fmaf(w[p], v, acc);
-  }
-  y[(size_t)t * H + n] = BF16 ? oc_f2bf(acc) : oc_f2h(acc);
-}
-
-struct MoePlan {
-  size_t h13_off, h_off, part_off, bytes;
+template <int BITS, int RM>
+struct MoeXch {  // x chunks per lane for RM rows of a unit
+  static constexpr int xc = (RM * 16 * Geo<BITS>::U + 63) / 64;
+  static constexpr int X = xc <= 1 ? 1 : (xc <= 4 ? 4 : (xc <= 8 ? 8 : 16));
 };
 
-MoePlan plan_moe(int M, int H, int I, int topk) {
+template <int BITS, int NT, int CS, int XCH>
+struct MoeD {  // units in flight per wave
+  static constexpr int DB = (BITS == 3 || BITS == 8) ? 2 : 4;
+  static constexpr int D = (XCH >= 8 || (CS == 1 && BITS == 3)) ? 1 : (DB / NT > 0 ? DB / NT : 1);
+};
+
+struct MoePlan {
+  size_t h_off, part_off, bytes;
+  int rm, w1, w2;
+  size_t lds1, lds2;
+};
+
+MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
   MoePlan p;
   const size_t pairs = (size_t)M * topk;
   const int h_pad = (H + 15) / 16 * 16;
-  p.h13_off = 0;
-  p.h_off = align256(pairs * 2 * I * 2);
-  p.part_off = p.h_off + align256(pairs * I * 2);
+  p.h_off = 0;
+  p.part_off = align256(pairs * I * 2);
   p.bytes = p.part_off + align256(pairs * h_pad * 4);
+  // rows per run: one for a single token (its slots name distinct experts); else 4, or 16
+  // when the pairs spread over the experts give more than 4 per expert on average
+  int rm = env_int("OC_MOE_RM", 0);
+  if (rm != 1 && rm != 4 && rm != 16) {
+    const size_t busy = pairs < (size_t)E ? pairs : (size_t)E;
+    rm = M == 1 ? 1 : ((pairs + busy - 1) / busy <= 4 ? 4 : 16);
+  }
+  if (pairs > 64) rm = 1;
+  p.rm = rm;
+  const int U = bits == 2 ? 2 : (bits == 3 ? 4 : 1);
+  const size_t slot = (size_t)rm * (128 * U + 8) * 2;
+  p.w1 = 4;  // gate|up
+  const int nu2 = (I + 128 * U - 1) / (128 * U);
+  // down: 8 waves for long k-ranges (runs of 1 or 4 rows, groups of 128 or more)
+  int w2 = env_int("OC_MOE_W2", 0);
+  if (w2 != 4 && w2 != 8) w2 = nu2 >= 24 ? 8 : 4;
+  if (rm == 16 || gs2 % 128 != 0) w2 = 4;
+  p.w2 = w2;
+  auto lds = [&](int w, int nt) {
+    const size_t xb = slot * w, rb = (size_t)w * nt * 256 * 4;
+    return ((xb > rb ? xb : rb) + 15) / 16 * 16;
+  };
+  p.lds1 = lds(p.w1, 2);
+  p.lds2 = lds(p.w2, 1);
   return p;
 }
 
-template <bool BF16>
-int launch_moe_gemv(const MoeGemvArgs& g, int bits, const GemvPlan& p, hipStream_t st) {
-  const dim3 grid((unsigned)(g.pairs * g.ngroups)), block(64 * p.w);
-#define OC_MG(B_, CS_, W_)                                                                              \
-  if (bits == B_ && p.cs == CS_ && p.w == W_) {                                                         \
-    hipLaunchKernelGGL((k_moe_gemv<B_, CS_, MoeDepth<B_, CS_>::D, W_, BF16>), grid, block, p.lds, st, g);   \
-    OC_HIP(hipGetLastError());                                                                          \
-    return 0;                                                                                           \
+template <bool BF16, bool UP>
+int launch_moe(const MoeArgs& g, int bits, int cs, int w, int rm, size_t lds, int grid, hipStream_t st) {
+#define OC_MK(B_, CS_, W_, RM_)                                                                            \
+  if (bits == B_ && cs == CS_ && w == W_ && rm == RM_) {                                                   \
+    constexpr int X_ = MoeXch<B_, RM_>::X;                                                                 \
+    constexpr int D_ = MoeD<B_, UP ? 2 : 1, CS_, X_>::D;                                                   \
+    if constexpr (UP)                                                                                      \
+      hipLaunchKernelGGL((k_moe_gate_up<B_, CS_, D_, W_, X_, RM_, BF16>), dim3(grid), dim3(64 * W_), lds,  \
+                         st, g);                                                                           \
+    else                                                                                                   \
+      hipLaunchKernelGGL((k_moe_down<B_, CS_, D_, W_, X_, RM_, BF16>), dim3(grid), dim3(64 * W_), lds, st, \
+                         g);                                                                               \
+    OC_HIP(hipGetLastError());                                                                             \
+    return 0;                                                                                              \
   }
-#define OC_MGB(B_) OC_MG(B_, 4, 16) OC_MG(B_, 4, 8) OC_MG(B_, 4, 4) OC_MG(B_, 1, 8) OC_MG(B_, 1, 4)
-  OC_MGB(2) OC_MGB(3) OC_MGB(4) OC_MGB(8)
-#undef OC_MGB
-#undef OC_MG
-  return oc::set_error(OC_ERR_UNSUPPORTED, "no MoE gemv kernel for bits=%d cs=%d w=%d", bits, p.cs, p.w);
+#define OC_MKR(B_, CS_, W_) OC_MK(B_, CS_, W_, 1) OC_MK(B_, CS_, W_, 4) OC_MK(B_, CS_, W_, 16)
+#define OC_MKB(B_) OC_MKR(B_, 4, 4) OC_MKR(B_, 1, 4)
+  OC_MKB(2) OC_MKB(3) OC_MKB(4) OC_MKB(8)
+  if constexpr (!UP) {  // longer k-ranges of down: 8 waves
+#define OC_MKW(B_) OC_MK(B_, 4, 8, 1) OC_MK(B_, 4, 8, 4)
+    OC_MKW(2) OC_MKW(3) OC_MKW(4) OC_MKW(8)
+#undef OC_MKW
+  }
+#undef OC_MKB
+#undef OC_MKR
+#undef OC_MK
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no MoE kernel for bits=%d cs=%d w=%d rows=%d", bits, cs, w, rm);
 }
 
 }  // namespace
 
 extern "C" size_t oc_moe_workspace_bytes(int M, int H, int I, int topk) {
   if (M <= 0 || H <= 0 || I <= 0 || topk <= 0) return 0;
-  return plan_moe(M, H, I, topk).bytes;
+  return plan_moe(M, H, I, 1, topk, 4, 128).bytes;
 }
 
 extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, int topk, const int32_t* ids,
@@ -1502,27 +1689,26 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   OC_REQUIRE(act_dtype == OC_DTYPE_F16 || act_dtype == OC_DTYPE_BF16, OC_ERR_UNSUPPORTED, "bad act_dtype %d",
              act_dtype);
   if (M == 0) return 0;
-  const MoePlan mp = plan_moe(M, H, I, topk);
+  OC_REQUIRE((size_t)M * topk * (I / 16) < (1u << 31) && (size_t)M * topk * ((H + 15) / 16) < (1u << 31),
+             OC_ERR_SHAPE, "M=%d x topk=%d is too large for one launch", M, topk);
+  const int gs13 = oc::eff_group(group_size, H), gs2 = oc::eff_group(group_size, I);
+  OC_REQUIRE(gs13 % 32 == 0 && gs2 % 32 == 0, OC_ERR_UNSUPPORTED, "group_size=%d", group_size);
+  const MoePlan mp = plan_moe(M, H, I, E, topk, bits, gs2);
   OC_REQUIRE(ws_bytes >= mp.bytes && workspace, OC_ERR_WORKSPACE,
              "workspace of %zu bytes is smaller than the %zu required", ws_bytes, mp.bytes);
   const oc::Layout L13 = oc::make_layout(bits, H, 2 * I), L2 = oc::make_layout(bits, I, H);
   OC_REQUIRE(w13_stride >= oc::layout_bytes(L13) && w2_stride >= oc::layout_bytes(L2), OC_ERR_INVALID,
              "expert strides smaller than one expert's packed weights");
-  const int gs13 = oc::eff_group(group_size, H), gs2 = oc::eff_group(group_size, I);
-  OC_REQUIRE(gs13 % 32 == 0 && gs2 % 32 == 0, OC_ERR_UNSUPPORTED, "group_size=%d", group_size);
   const int G13 = (H + gs13 - 1) / gs13, G2 = (I + gs2 - 1) / gs2;
   OC_REQUIRE(meta13_stride >= (size_t)G13 * L13.N_pad && meta2_stride >= (size_t)G2 * L2.N_pad, OC_ERR_INVALID,
              "expert scale/zero strides too small");
   hipStream_t st = (hipStream_t)stream;
   const bool bf16 = act_dtype == OC_DTYPE_BF16;
   uint8_t* ws = (uint8_t*)workspace;
-  uint16_t* h13 = (uint16_t*)(ws + mp.h13_off);
-  uint16_t* h = (uint16_t*)(ws + mp.h_off);
-  float* part = (float*)(ws + mp.part_off);
   const int pairs = M * topk;
   auto fill = [&](GemvArgs& a, const oc::Layout& L, int K, int N, int gs, int G) {
     a = GemvArgs{};
-    a.M = 1;
+    a.M = mp.rm;
     a.K = K;
     a.N = N;
     a.N_pad = L.N_pad;
@@ -1535,75 +1721,54 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
     a.ups = L.NU;
     a.bits = bits;
   };
-  // 1. gate | up for every pair
-  {
-    const GemvPlan p = plan_gemv(L13, 1, gs13);
-    MoeGemvArgs g = {};
-    fill(g.base, L13, H, 2 * I, gs13, G13);
-    g.base.x = (const uint16_t*)x;
-    g.base.w = (const uint8_t*)w13;
-    g.base.meta = meta13;
-    g.base.bias = (const uint16_t*)b13;
-    g.base.y = h13;
-    g.base.ldy = 2 * I;
-    g.ids = ids;
-    g.pairs = pairs;
-    g.topk = topk;
-    g.E = E;
-    g.x_per_pair = 0;
-    g.w_stride = w13_stride;
-    g.meta_stride = meta13_stride;
-    g.bias_stride = 2 * I;
-    g.y_stride = 2 * I;
-    g.ngroups = L13.NT;
-    GemvPlan q = p;
-    q.nt = 1;
-    const int rc = bf16 ? launch_moe_gemv<true>(g, bits, q, st) : launch_moe_gemv<false>(g, bits, q, st);
-    if (rc) return rc;
-  }
-  // 2. activation
-  {
-    const dim3 grid((I + 255) / 256, pairs);
-    if (bf16) hipLaunchKernelGGL(k_moe_act<true>, grid, dim3(256), 0, st, h13, I, pairs, act, alpha, limit, ids, E, h);
-    else hipLaunchKernelGGL(k_moe_act<false>, grid, dim3(256), 0, st, h13, I, pairs, act, alpha, limit, ids, E, h);
-    OC_HIP(hipGetLastError());
-  }
-  // 3. down for every pair, fp32
-  {
-    const GemvPlan p = plan_gemv(L2, 1, gs2);
-    MoeGemvArgs g = {};
-    fill(g.base, L2, I, H, gs2, G2);
-    g.base.x = h;
-    g.base.w = (const uint8_t*)w2;
-    g.base.meta = meta2;
-    g.base.partial = part;
-    g.base.out_f32 = 1;
-    g.base.ldy = H;
-    g.ids = ids;
-    g.pairs = pairs;
-    g.topk = topk;
-    g.E = E;
-    g.x_per_pair = 1;
-    g.w_stride = w2_stride;
-    g.meta_stride = meta2_stride;
-    g.bias_stride = 0;
-    g.y_stride = L2.N_pad;
-    g.ngroups = L2.NT;
-    GemvPlan q = p;
-    q.nt = 1;
-    const int rc = bf16 ? launch_moe_gemv<true>(g, bits, q, st) : launch_moe_gemv<false>(g, bits, q, st);
-    if (rc) return rc;
-  }
-  // 4. weighted sum over the top-k (+ down bias)
-  {
-    const dim3 grid((H + 255) / 256, M);
-    if (bf16)
-      hipLaunchKernelGGL(k_moe_combine<true>, grid, dim3(256), 0, st, part, H, L2.N_pad, topk, M, ids, E, weights,
-                         (const uint16_t*)b2, (uint16_t*)y);
-    else
-      hipLaunchKernelGGL(k_moe_combine<false>, grid, dim3(256), 0, st, part, H, L2.N_pad, topk, M, ids, E, weights,
-                         (const uint16_t*)b2, (uint16_t*)y);
-    OC_HIP(hipGetLastError());
-  }
+  MoeArgs g = {};
+  g.ids = ids;
+  g.pairs = pairs;
+  g.topk = topk;
+  g.E = E;
+  g.I = I;
+  g.act = act;
+  g.alpha = alpha;
+  g.limit = limit;
+  uint16_t* h = (uint16_t*)(ws + mp.h_off);
+  // 1. gate | up and the activation
+  fill(g.base, L13, H, 2 * I, gs13, G13);
+  g.base.x = (const uint16_t*)x;
+  g.base.w = (const uint8_t*)w13;
+  g.base.meta = meta13;
+  g.bias = (const uint16_t*)b13;
+  g.out = h;
+  g.part = nullptr;
+  g.ntiles = I / 16;
+  g.w_stride = w13_stride;
+  g.meta_stride = meta13_stride;
+  const int cs13 = (gs13 % 128) == 0 ? 4 : 1, cs2 = (gs2 % 128) == 0 ? 4 : 1;
+  int rc = bf16 ? launch_moe<true, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, pairs * g.ntiles, st)
+                : launch_moe<false, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, pairs * g.ntiles, st);
+  if (rc) return rc;
+  // 2. down per run, fp32 sums per pair
+  fill(g.base, L2, I, H, gs2, G2);
+  g.base.x = h;
+  g.base.w = (const uint8_t*)w2;
+  g.base.meta = meta2;
+  g.bias = nullptr;
+  g.out = nullptr;
+  g.ntiles = L2.NT;
+  g.w_stride = w2_stride;
+  g.meta_stride = meta2_stride;
+  float* part = (float*)(ws + mp.part_off);
+  g.part = part;
+  rc = bf16 ? launch_moe<true, false>(g, bits, cs2, mp.w2, mp.rm, mp.lds2, pairs * g.ntiles, st)
+            : launch_moe<false, false>(g, bits, cs2, mp.w2, mp.rm, mp.lds2, pairs * g.ntiles, st);
+  if (rc) return rc;
+  // 3. weighted sum over the top-k (+ down bias)
+  const dim3 grid((H + 255) / 256, M);
+  if (bf16)
+    hipLaunchKernelGGL(k_moe_combine<true>, grid, dim3(256), 0, st, part, H, L2.N_pad, topk, M, ids, E, weights,
+                       (const uint16_t*)b2, (uint16_t*)y);
+  else
+    hipLaunchKernelGGL(k_moe_combine<false>, grid, dim3(256), 0, st, part, H, L2.N_pad, topk, M, ids, E, weights,
+                       (const uint16_t*)b2, (uint16_t*)y);
+  OC_HIP(hipGetLastError());
   return 0;
 }

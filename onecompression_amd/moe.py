@@ -20,6 +20,7 @@ travels to the host.  :class:`GPTQExperts` is the HF-path drop-in with
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -52,9 +53,9 @@ class PreparedExperts:
 def _prepare_into(qweight, qzeros, scales, bits, group_size, zero_format, packed, meta):
     k, n = qweight.shape[0] * 32 // bits, qweight.shape[1]
     g = scales.shape[0]
-    ident = __import__("ctypes").c_int(1)
+    ident = ctypes.c_int(1)
     N.call("oc_gptq_prepare", _ptr(qweight), _ptr(qzeros), _ptr(scales), None, k, n, g, bits, group_size,
-           zero_format, _ptr(packed), _ptr(meta), None, __import__("ctypes").byref(ident), _stream(qweight.device))
+           zero_format, _ptr(packed), _ptr(meta), None, ctypes.byref(ident), _stream(qweight.device))
 
 
 def prepare_experts(gate: Sequence, up: Sequence, down: Sequence, bits: int, group_size: int,

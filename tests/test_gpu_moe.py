@@ -119,3 +119,58 @@ def test_gptq_experts_module_forward(dev):
     want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
     err = float(np.max(np.abs(y1.float().cpu().numpy() - want)) / np.max(np.abs(want)))
     assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("m,k,E", [(6, 3, 4), (40, 2, 6), (17, 4, 5)])
+def test_moe_shared_experts_duplicates_and_empty_tokens(dev, m, k, E):
+    """Runs of several tokens on one expert (pairs <= 64), one row per pair (pairs > 64), a token
+    that names one expert twice, and a token whose every slot is invalid (its output is zero)."""
+    H, I, gs, bits = 256, 64, 64, 4
+    cases, ref = _build(E, H, I, bits, gs, True, "fp16", seed=31 + m)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=9)
+    g = torch.Generator().manual_seed(m)
+    idx = torch.randint(0, E, (m, k), generator=g, dtype=torch.int32)
+    idx[0, :] = 1
+    idx[1, :] = -1
+    idx[2, 0] = E + 3
+    w = torch.softmax(torch.randn(m, k, generator=g), dim=-1)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "silu").float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
+    assert np.all(y[1] == 0.0)
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
+    # a second call on the same workspace state gives the same bytes (the counters reset)
+    y2 = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "silu").float().cpu().numpy()
+    assert np.array_equal(y, y2)
+
+
+@pytest.mark.parametrize("bits,inter", [(4, 3072), (4, 8192), (2, 8192), (3, 8192), (8, 4096)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_moe_long_down(dev, bits, inter, m):
+    """Long down k-ranges take 8 or 16 waves per workgroup."""
+    E, H, k, gs = 3, 128, 2, 128
+    cases, ref = _build(E, H, inter, bits, gs, False, "fp16", seed=50 + bits)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=12)
+    idx, w = _routing(m, k, E, seed=13)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "silu").float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("rows", [4, 16])
+def test_moe_runs_of_rows(dev, monkeypatch, bits, rows):
+    """Runs of up to 4 or 16 pairs on one expert (OC_MOE_RM forces the run length)."""
+    monkeypatch.setenv("OC_MOE_RM", str(rows))
+    E, H, I, k, gs, m = 3, 256, 128, 2, 128, 20
+    cases, ref = _build(E, H, I, bits, gs, True, "fp16", seed=70 + bits)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=14)
+    idx, w = _routing(m, k, E, seed=15)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "gpt_oss").float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
