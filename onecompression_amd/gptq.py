@@ -46,6 +46,7 @@ from .vllm_compat import (
     LinearBase,
     LinearMethodBase,
     QuantizationConfig,
+    QuantizeMethodBase,
     UnquantizedLinearMethod,
     register_quantization_config,
     set_weight_attrs,
@@ -324,6 +325,108 @@ def _zero_loader(loader, offs, parts, bits):
     return _load
 
 
+class GPTQMoEMethod(QuantizeMethodBase):
+    """FusedMoE method over GPTQ experts.
+
+    Replaces the vLLM WNA16 method that ``MixedGPTQConfig._get_moe_quant_method`` builds
+    (vllm_plugins/gptq/vllm_plugin.py:241-283) and its gpt-oss variant with expert bias and the
+    swigluoai activation (gptoss_wna16_moe.py:55-175).  The experts' AutoGPTQ tensors are
+    registered expert-stacked, gate and up side by side (gate columns first):
+    ``w13_qweight`` [E, H·b/32, 2I], ``w13_qzeros`` [E, G, 2I·b/32], ``w13_scales`` [E, G, 2I],
+    ``w2_*`` likewise for down (I -> H), and with ``layer.has_bias`` ``w13_bias`` [E, 2I],
+    ``w2_bias`` [E, H].  The loader takes FusedMoE's ``(param, loaded, weight_name, shard_id,
+    expert_id)`` with shard_id ``w1`` (gate), ``w3`` (up) or ``w2`` (down).  After loading the
+    experts are repacked once (``moe.prepare_experts_merged``) and the checkpoint tensors freed;
+    ``apply`` runs ``oc_moe_gptq_forward``.
+    """
+
+    _ACT = {"silu": "silu", "swigluoai": "gpt_oss", "gelu": "gelu_pytorch_tanh"}
+
+    def __init__(self, quant_config: GPTQLayerConfig):
+        if quant_config.desc_act:
+            raise NotImplementedError("act-order (desc_act) MoE experts are not supported")
+        self.quant_config = quant_config
+
+    def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
+                       intermediate_size_per_partition: int, params_dtype: torch.dtype, **extra_weight_attrs):
+        cfg = self.quant_config
+        bits, E, H, I = cfg.weight_bits, num_experts, hidden_size, intermediate_size_per_partition
+        if H % 32 or I % 32:
+            raise ValueError(f"hidden {H} and intermediate {I} sizes must be multiples of 32")
+        gs13 = cfg.group_size if cfg.group_size != -1 else H
+        gs2 = cfg.group_size if cfg.group_size != -1 else I
+        if gs13 % 32 or gs2 % 32:
+            raise ValueError(f"group_size {cfg.group_size} must be a multiple of 32 (or -1)")
+        g13, g2 = (H + gs13 - 1) // gs13, (I + gs2 - 1) // gs2
+        extra_weight_attrs.pop("weight_loader", None)
+        shapes = {
+            "w13_qweight": ((E, H * bits // 32, 2 * I), torch.int32),
+            "w13_qzeros": ((E, g13, 2 * I * bits // 32), torch.int32),
+            "w13_scales": ((E, g13, 2 * I), torch.float16),
+            "w2_qweight": ((E, I * bits // 32, H), torch.int32),
+            "w2_qzeros": ((E, g2, H * bits // 32), torch.int32),
+            "w2_scales": ((E, g2, H), torch.float16),
+        }
+        if getattr(layer, "has_bias", False):
+            shapes["w13_bias"] = ((E, 2 * I), params_dtype)
+            shapes["w2_bias"] = ((E, H), params_dtype)
+        for name, (shape, dtype) in shapes.items():
+            param = torch.nn.Parameter(torch.zeros(shape, dtype=dtype), requires_grad=False)
+            layer.register_parameter(name, param)
+            set_weight_attrs(param, {"weight_loader": self._load, **extra_weight_attrs})
+        layer._oc_moe = {"E": E, "H": H, "I": I}
+
+    @staticmethod
+    def _load(param, loaded_weight: torch.Tensor, weight_name: str, shard_id: str, expert_id: int,
+              return_success: bool = False):
+        """Place one expert's gate (w1) / up (w3) half of a w13 tensor, or its down (w2) tensor."""
+        dst = param.data[expert_id]
+        if "w13" in weight_name:
+            if shard_id not in ("w1", "w3"):
+                raise ValueError(f"{weight_name}: shard_id must be w1 or w3, got {shard_id!r}")
+            half = dst.shape[-1] // 2
+            dst = dst.narrow(dst.dim() - 1, 0 if shard_id == "w1" else half, half)
+        elif shard_id != "w2":
+            raise ValueError(f"{weight_name}: shard_id must be w2, got {shard_id!r}")
+        if tuple(loaded_weight.shape) != tuple(dst.shape):
+            raise ValueError(f"{weight_name} expert {expert_id} shard {shard_id}: checkpoint shape "
+                             f"{tuple(loaded_weight.shape)} != {tuple(dst.shape)}")
+        dst.copy_(loaded_weight.to(device=dst.device, dtype=dst.dtype))
+        return True if return_success else None
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        from . import moe
+
+        cfg = self.quant_config
+        if layer.w13_qweight.device.type != "cuda":
+            raise RuntimeError("GPTQMoEMethod needs the layer on a HIP device before process_weights_after_loading")
+        b13 = getattr(layer, "w13_bias", None)
+        b2 = getattr(layer, "w2_bias", None)
+        layer._oc_experts = moe.prepare_experts_merged(
+            layer.w13_qweight.data, layer.w13_qzeros.data, layer.w13_scales.data, layer.w2_qweight.data,
+            layer.w2_qzeros.data, layer.w2_scales.data, cfg.weight_bits, cfg.group_size, cfg.zero_format,
+            None if b13 is None else b13.data, None if b2 is None else b2.data)
+        for name in ("w13_qweight", "w13_qzeros", "w13_scales", "w2_qweight", "w2_qzeros", "w2_scales"):
+            getattr(layer, name).data = torch.empty(0, dtype=getattr(layer, name).dtype,
+                                                    device=layer.w13_qweight.device)
+
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor, topk_weights: torch.Tensor,
+              topk_ids: torch.Tensor, shared_experts_input: Optional[torch.Tensor] = None) -> torch.Tensor:
+        from . import moe
+
+        ex = getattr(layer, "_oc_experts", None)
+        if ex is None:
+            raise RuntimeError("GPTQ MoE layer used before process_weights_after_loading")
+        if getattr(layer, "apply_router_weight_on_input", False):
+            raise NotImplementedError("apply_router_weight_on_input is not supported")
+        if getattr(layer, "expert_map", None) is not None:
+            raise NotImplementedError("expert parallelism (expert_map) is not supported")
+        act = str(getattr(layer, "activation", "silu")).lower().rsplit(".", 1)[-1]
+        if act not in self._ACT:
+            raise NotImplementedError(f"MoE activation {act!r}; supported: {sorted(self._ACT)}")
+        return moe.moe_forward(x, topk_ids, topk_weights, ex, self._ACT[act])
+
+
 @register_quantization_config("mixed_gptq")
 class MixedGPTQConfig(QuantizationConfig):
     """``quant_method: mixed_gptq`` (vllm_plugins/gptq/vllm_plugin.py:83-365)."""
@@ -418,11 +521,39 @@ class MixedGPTQConfig(QuantizationConfig):
         return maybe_wrap_rotation_method(UnquantizedLinearMethod(), prefix=prefix,
                                           metadata=self.rotation_metadata)
 
+    def _lookup_moe_expert_config(self, layer_idx: int) -> Optional[Dict[str, Any]]:
+        """A representative per-expert GPTQ entry of a MoE layer: gate_proj first, then up, down,
+        then any expert projection (vllm_plugin.py:220-239; all experts share bits/group size)."""
+        if layer_idx >= len(self.quantization_bits):
+            return None
+        layer_cfg = self.quantization_bits[layer_idx]
+        for suffix in (".gate_proj", ".up_proj", ".down_proj"):
+            for name, cfg in layer_cfg.items():
+                if _MOE_EXPERT_CFG_RE.search(name) and name.endswith(suffix):
+                    return cfg
+        for name, cfg in layer_cfg.items():
+            if _MOE_EXPERT_CFG_RE.search(name):
+                return cfg
+        return None
+
+    def _get_moe_quant_method(self, layer: torch.nn.Module, prefix: str):
+        """GPTQMoEMethod for a FusedMoE layer with per-expert GPTQ entries, else None (unquantized
+        experts), as vllm_plugin.py:241-283 decides."""
+        layer_idx, _ = parse_layer_and_module(prefix)
+        if layer_idx is None:
+            return None
+        mod_cfg = self._lookup_moe_expert_config(layer_idx)
+        if mod_cfg is None:
+            return None
+        bits = int(mod_cfg.get("bits", 0))
+        if bits == 0 or mod_cfg.get("method", "gptq") != "gptq":
+            return None
+        return GPTQMoEMethod(GPTQLayerConfig(bits, self.resolve_group_size(mod_cfg), self.desc_act,
+                                             bool(self.sym), self.checkpoint_format))
+
     def get_quant_method(self, layer: torch.nn.Module, prefix: str):
         if FusedMoE is not None and isinstance(layer, FusedMoE):
-            raise NotImplementedError(
-                "onecomp-amd serves dense GPTQ linears only; the GPT-OSS / Qwen MoE WNA16 "
-                "expert path (vllm_plugins/gptq/gptoss_wna16_moe.py) is not part of this build")
+            return self._get_moe_quant_method(layer, prefix)
         if not isinstance(layer, LinearBase):
             return None
         layer_idx, suffix = parse_layer_and_module(prefix)

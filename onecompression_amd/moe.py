@@ -58,6 +58,30 @@ def _prepare_into(qweight, qzeros, scales, bits, group_size, zero_format, packed
            zero_format, _ptr(packed), _ptr(meta), None, ctypes.byref(ident), _stream(qweight.device))
 
 
+def _prepare(E, H, I, bits, group_size, zero_format, w13_of, w2_of, b13, b2, dev) -> PreparedExperts:
+    if I * bits % 32:
+        raise ValueError(f"intermediate size {I} x {bits} bits does not pack the merged gate|up zeros")
+    nb13, _, np13 = gptq_layout(H, 2 * I, bits)
+    nb2, _, np2 = gptq_layout(I, H, bits)
+    gs13 = group_size if group_size > 0 else H
+    gs2 = group_size if group_size > 0 else I
+    g13, g2 = (H + gs13 - 1) // gs13, (I + gs2 - 1) // gs2
+    w13 = torch.empty((E, nb13), dtype=torch.uint8, device=dev)
+    meta13 = torch.empty((E, g13 * np13), dtype=torch.int32, device=dev)
+    w2 = torch.empty((E, nb2), dtype=torch.uint8, device=dev)
+    meta2 = torch.empty((E, g2 * np2), dtype=torch.int32, device=dev)
+    for e in range(E):
+        qw, qz, sc = w13_of(e)
+        _need(qw, "gate|up qweight", torch.int32, dev=dev)
+        _prepare_into(qw.contiguous(), qz.contiguous(), sc.to(torch.float16).contiguous(), bits, group_size,
+                      zero_format, w13[e], meta13[e])
+        qw, qz, sc = w2_of(e)
+        _need(qw, "down qweight", torch.int32, dev=dev)
+        _prepare_into(qw.contiguous(), qz.contiguous(), sc.to(torch.float16).contiguous(), bits, group_size,
+                      zero_format, w2[e], meta2[e])
+    return PreparedExperts(w13, meta13, b13, w2, meta2, b2, E, H, I, bits, group_size)
+
+
 def prepare_experts(gate: Sequence, up: Sequence, down: Sequence, bits: int, group_size: int,
                     zero_format: int = N.OC_ZERO_V1, gate_up_bias: Optional[Sequence] = None,
                     down_bias: Optional[Sequence] = None) -> PreparedExperts:
@@ -72,30 +96,30 @@ def prepare_experts(gate: Sequence, up: Sequence, down: Sequence, bits: int, gro
     dev = gate[0][0].device
     H = gate[0][0].shape[0] * 32 // bits
     I = gate[0][0].shape[1]
-    if I * bits % 32:
-        raise ValueError(f"intermediate size {I} x {bits} bits does not pack the merged gate|up zeros")
-    nb13, _, np13 = gptq_layout(H, 2 * I, bits)
-    nb2, _, np2 = gptq_layout(I, H, bits)
-    gs13 = group_size if group_size > 0 else H
-    gs2 = group_size if group_size > 0 else I
-    g13, g2 = (H + gs13 - 1) // gs13, (I + gs2 - 1) // gs2
-    w13 = torch.empty((E, nb13), dtype=torch.uint8, device=dev)
-    meta13 = torch.empty((E, g13 * np13), dtype=torch.int32, device=dev)
-    w2 = torch.empty((E, nb2), dtype=torch.uint8, device=dev)
-    meta2 = torch.empty((E, g2 * np2), dtype=torch.int32, device=dev)
-    for e in range(E):
-        (gq, gz, gsc), (uq, uz, usc), (dq, dz, dsc) = gate[e], up[e], down[e]
-        for t, name in ((gq, "gate qweight"), (uq, "up qweight"), (dq, "down qweight")):
-            _need(t, name, torch.int32, dev=dev)
-        qw = torch.cat([gq, uq], dim=1).contiguous()
-        qz = torch.cat([gz, uz], dim=1).contiguous()
-        sc = torch.cat([gsc, usc], dim=1).to(torch.float16).contiguous()
-        _prepare_into(qw, qz, sc, bits, group_size, zero_format, w13[e], meta13[e])
-        _prepare_into(dq.contiguous(), dz.contiguous(), dsc.to(torch.float16).contiguous(), bits, group_size,
-                      zero_format, w2[e], meta2[e])
+
+    def w13_of(e):
+        (gq, gz, gsc), (uq, uz, usc) = gate[e], up[e]
+        return torch.cat([gq, uq], dim=1), torch.cat([gz, uz], dim=1), torch.cat([gsc, usc], dim=1)
+
     b13 = None if gate_up_bias is None else torch.stack([b.reshape(-1) for b in gate_up_bias]).contiguous()
     b2 = None if down_bias is None else torch.stack([b.reshape(-1) for b in down_bias]).contiguous()
-    return PreparedExperts(w13, meta13, b13, w2, meta2, b2, E, H, I, bits, group_size)
+    return _prepare(E, H, I, bits, group_size, zero_format, w13_of, lambda e: down[e], b13, b2, dev)
+
+
+def prepare_experts_merged(w13_qweight: torch.Tensor, w13_qzeros: torch.Tensor, w13_scales: torch.Tensor,
+                           w2_qweight: torch.Tensor, w2_qzeros: torch.Tensor, w2_scales: torch.Tensor, bits: int,
+                           group_size: int, zero_format: int = N.OC_ZERO_V1, w13_bias: Optional[torch.Tensor] = None,
+                           w2_bias: Optional[torch.Tensor] = None) -> PreparedExperts:
+    """Expert-stacked AutoGPTQ tensors of a FusedMoE layer: w13_* [E, ...] hold each expert's gate
+    and up side by side (gate columns first), w2_* its down; biases [E, 2I] and [E, H] or None."""
+    E = w13_qweight.shape[0]
+    H = w13_qweight.shape[1] * 32 // bits
+    I = w13_qweight.shape[2] // 2
+    return _prepare(E, H, I, bits, group_size, zero_format,
+                    lambda e: (w13_qweight[e], w13_qzeros[e], w13_scales[e]),
+                    lambda e: (w2_qweight[e], w2_qzeros[e], w2_scales[e]),
+                    None if w13_bias is None else w13_bias.contiguous(),
+                    None if w2_bias is None else w2_bias.contiguous(), w13_qweight.device)
 
 
 def moe_forward(x: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor, ex: PreparedExperts,

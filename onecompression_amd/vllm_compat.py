@@ -1,7 +1,7 @@
 """vLLM plugin base classes, or local stand-ins when vLLM is not installed.
 
 When ``vllm`` is importable the real ``QuantizationConfig``,
-``LinearMethodBase``, ``LinearBase``, ``UnquantizedLinearMethod``,
+``LinearMethodBase``, ``LinearBase``, ``UnquantizedLinearMethod``, ``FusedMoE``,
 ``set_weight_attrs`` and ``register_quantization_config`` are re-exported, so
 the configs in this package register with a real vLLM exactly like
 ``vllm_plugins/gptq`` and ``vllm_plugins/dbf`` do (pyproject.toml:105-107).
@@ -36,7 +36,6 @@ try:  # pragma: no cover - exercised only where vLLM is installed
     HAS_VLLM = True
 except Exception:  # noqa: BLE001 - any import failure means "no vLLM"
     HAS_VLLM = False
-    FusedMoE = None
 
     class QuantizeMethodBase:
         """Stand-in for vllm...base_config.QuantizeMethodBase."""
@@ -127,6 +126,43 @@ except Exception:  # noqa: BLE001 - any import failure means "no vLLM"
 
         def apply(self, layer, x, bias=None):
             return F.linear(x, layer.weight, bias)
+
+    class FusedMoE(torch.nn.Module):
+        """Minimal MoE experts layer in vLLM's style: the quant method owns the expert params
+        (``create_weights(layer, num_experts, hidden_size, intermediate_size_per_partition,
+        params_dtype)``), the weight loader takes ``(param, loaded, weight_name, shard_id,
+        expert_id)`` with shard_id ``w1`` (gate), ``w3`` (up) or ``w2`` (down), and forward
+        takes the router's top-k weights and ids.  ``activation``: ``"silu"`` or
+        ``"swigluoai"`` (gpt-oss)."""
+
+        def __init__(self, num_experts: int, top_k: int, hidden_size: int, intermediate_size: int,
+                     params_dtype: torch.dtype = torch.float16,
+                     quant_config: Optional["QuantizationConfig"] = None, prefix: str = "",
+                     activation: str = "silu", has_bias: bool = False):
+            super().__init__()
+            self.global_num_experts = num_experts
+            self.top_k = top_k
+            self.hidden_size = hidden_size
+            self.intermediate_size_per_partition = intermediate_size
+            self.params_dtype = params_dtype
+            self.prefix = prefix
+            self.activation = activation
+            self.has_bias = has_bias
+            self.apply_router_weight_on_input = False
+            self.expert_map = None
+            self.quant_method = None if quant_config is None else quant_config.get_quant_method(self, prefix)
+            if self.quant_method is None:
+                raise NotImplementedError("the stand-in FusedMoE serves quantized experts only")
+            self.quant_method.create_weights(self, num_experts, hidden_size, intermediate_size, params_dtype,
+                                             weight_loader=self.weight_loader)
+
+        def weight_loader(self, param, loaded_weight, weight_name: str, shard_id: str, expert_id: int,
+                          return_success: bool = False):
+            return param.weight_loader(param, loaded_weight, weight_name, shard_id, expert_id, return_success)
+
+        def forward(self, hidden_states: torch.Tensor, topk_weights: torch.Tensor,
+                    topk_ids: torch.Tensor) -> torch.Tensor:
+            return self.quant_method.apply(self, hidden_states, topk_weights, topk_ids, None)
 
     def set_weight_attrs(weight: torch.Tensor, weight_attrs: Optional[Dict[str, Any]]) -> None:
         if weight_attrs is None:

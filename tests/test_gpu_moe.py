@@ -174,3 +174,41 @@ def test_moe_runs_of_rows(dev, monkeypatch, bits, rows):
     want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss")
     err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
     assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("act,bits", [("silu", 4), ("swigluoai", 3)])
+def test_vllm_fused_moe_layer(dev, act, bits):
+    """MixedGPTQConfig -> FusedMoE -> GPTQMoEMethod: load the experts shard by shard, process,
+    forward (the path vllm_plugin.py:241-283 hands to vLLM's WNA16 method)."""
+    from onecompression_amd import gptq as G
+    from onecompression_amd.vllm_compat import HAS_VLLM, FusedMoE
+
+    if HAS_VLLM:
+        pytest.skip("uses the stand-in FusedMoE")
+    E, H, I, k, gs, m = 4, 256, 128, 2, 128, 5
+    qb = [{f"mlp.experts.{e}.{p}": {"bits": bits, "method": "gptq", "group_size": gs}
+           for e in range(E) for p in ("gate_proj", "up_proj", "down_proj")}]
+    cfg = G.MixedGPTQConfig(quantization_bits=qb, group_size=-1, desc_act=False, sym=False,
+                            checkpoint_format="gptq")
+    bias = act == "swigluoai"
+    layer = FusedMoE(E, k, H, I, quant_config=cfg, prefix="model.layers.0.mlp.experts", activation=act,
+                     has_bias=bias)
+    cases, ref = _build(E, H, I, bits, gs, bias, "fp16", seed=90 + bits)
+    for e, (g, u, d, bs) in enumerate(cases):
+        for sid, c in (("w1", g), ("w3", u), ("w2", d)):
+            pre = "w2" if sid == "w2" else "w13"
+            for t in ("qweight", "qzeros", "scales"):
+                layer.weight_loader(getattr(layer, f"{pre}_{t}"), getattr(c, t), f"experts.{pre}_{t}", sid, e)
+        if bias:
+            layer.weight_loader(layer.w13_bias, bs[0], "experts.w13_bias", "w1", e)
+            layer.weight_loader(layer.w13_bias, bs[1], "experts.w13_bias", "w3", e)
+            layer.weight_loader(layer.w2_bias, bs[2], "experts.w2_bias", "w2", e)
+    layer.to(dev)
+    layer.quant_method.process_weights_after_loading(layer)
+    assert layer.w13_qweight.numel() == 0  # checkpoint tensors freed after the repack
+    x = synth.activations(m, H, torch.float16, seed=17)
+    idx, w = _routing(m, k, E, seed=18)
+    y = layer(x.to(dev), w.to(dev), idx.to(dev)).float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss" if bias else "silu")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
