@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 3
+#define OC_ABI_VERSION 4
 
 enum {
   OC_OK = 0,

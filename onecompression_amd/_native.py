@@ -49,7 +49,7 @@ SIGNATURES = {
     "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, c_size_t, P]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
 OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2
 ERR_NAMES = {-1: "INVALID", -2: "UNSUPPORTED", -3: "SHAPE", -4: "HIP", -5: "WORKSPACE", -6: "GIDX"}
