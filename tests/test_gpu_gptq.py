@@ -272,6 +272,24 @@ def test_gemm_streaming_variants(dev, bits, case, monkeypatch):
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=95 + bits), 5, "fp16", bias=True)
 
 
+# The streaming GEMV folds the zero point in through per-k-block sums of x (an fp32 offset term
+# of 1024 sum(x) that cancels): tiny activations and a wide dynamic range stay within the bar.
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("scale", ["tiny", "wide"])
+def test_gemm_streaming_3bit_small_and_wide_x(dev, m, scale):
+    c = _case(1024, 16384, 3, seed=170 + m)
+    cd = c.to(dev)
+    prep = ops.gptq_prepare(cd.qweight, cd.qzeros, cd.scales, None, 3, 128)
+    g = torch.Generator().manual_seed(171 + m)
+    x = torch.randn((m, 1024), generator=g)
+    x = x * 1e-3 if scale == "tiny" else x * torch.pow(10.0, torch.empty((m, 1024)).uniform_(-4, 2, generator=g))
+    x = x.to(torch.float16)
+    y = ops.gptq_gemm(x.to(dev), prep)
+    ref = og.linear_ref(_np(x), _oracle_w(c, "fp16"), "fp16", None)
+    r = _rel(_np(y.float()), ref)
+    assert r <= 1e-2, f"max rel err {r:.3e}"
+
+
 # Wide layers at mid M take the streaming GEMM (k-block x staging ring, MB row blocks per B
 # operand); K = 14336 at M = 4 takes it too (x does not fit the GEMV stream's LDS).
 @pytest.mark.parametrize("bits", BITS)
