@@ -178,8 +178,8 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
 RIDGE_FLOP_PER_BYTE = MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
 # MoE blocks with GPTQ experts (not a BASELINE config): name, hidden, intermediate, experts, top-k, Ms
-MOE_SHAPES = [("Qwen3-30B-A3B experts", 2048, 768, 128, 8, (1, 8)),
-              ("Mixtral-8x7B experts", 4096, 14336, 8, 2, (1, 4))]
+MOE_SHAPES = [("Qwen3-30B-A3B experts", 2048, 768, 128, 8, (1, 8, 256)),
+              ("Mixtral-8x7B experts", 4096, 14336, 8, 2, (1, 4, 64))]
 
 
 def report_moe(dev, bits=4, gs=128, routings=16):

@@ -154,8 +154,9 @@ size_t oc_moe_workspace_bytes(int M, int H, int I, int topk);
  * first), w13_stride bytes apart; meta13 their scale/zero words, meta13_stride words apart; b13
  * [E, 2I] or NULL.  w2 / meta2 / b2 likewise for down (I -> H).  x [M, H], y [M, H] in act_dtype.
  * Three launches on `stream` (gate|up with the activation, down, the top-k sum), no host
- * synchronisation, no allocation.  Pairs that share an expert (up to 64 pairs per call) share
- * one read of its weights, up to 16 at a time.
+ * synchronisation, no allocation.  Pairs that share an expert share one read of its weights,
+ * up to 16 at a time; beyond 64 pairs a fourth launch first sorts the pairs by expert
+ * (E <= 2048; above that every pair reads its expert).
  * Replaces _UnfusedExperts.forward, onecomp/utils/unfuse_moe.py:61-114 (with the gpt-oss combine
  * of :380-387) over GPTQ experts, and the WNA16 fused-experts dispatch of
  * vllm_plugins/gptq/vllm_plugin.py:240-283. */

@@ -340,11 +340,21 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, const int block) {
 // workgroups of the first pair of each run read e's weights once for all the
 // run's rows (the rows of the MFMA A operand); the other pairs' workgroups
 // exit.  With RM = 1 every pair is its own run.  RM > 1 needs pairs <= 64
-// (one id per lane of a wave).
+// (one id per lane of a wave).  RM = kMoeSorted: k_moe_sort has put the pairs
+// in expert order and cut them into runs of at most 16; workgroup group r
+// serves run r of that table (any number of pairs).
 // ---------------------------------------------------------------------------
+constexpr int kMoeSorted = 0;
+constexpr int kMoeMaxE = 2048;  // experts the sort handles (its LDS tables)
+
+__host__ __device__ constexpr int moe_cap(int RM) { return RM == kMoeSorted ? 16 : RM; }
+
 struct MoeArgs {
-  GemvArgs base;        // the layer's shape; M = RM (x slot rows); w / meta = expert 0
+  GemvArgs base;        // the layer's shape; M = rows per run (x slot rows); w / meta = expert 0
   const int32_t* ids;   // [pairs]
+  const int* runs;      // sorted runs: [runs][4] = expert, first index into sorted, rows, 0
+  const int* sorted;    // sorted runs: pair indices in expert order
+  const int* nruns;     // sorted runs: number of runs
   const uint16_t* bias; // gate|up bias [E, 2I], or null
   uint16_t* out;        // gate|up launch: h [pairs, I]
   float* part;          // down launch: fp32 sums per pair [pairs, N_pad]
@@ -359,15 +369,25 @@ struct MoeArgs {
 struct MoeRun {
   int e;          // expert of the workgroup's pair
   int rows;       // rows this workgroup serves (0: none)
-  uint64_t mask;  // pairs of the run and of later runs of e (bit q = pair q), RM > 1 only
+  uint64_t mask;  // pairs of the run and of later runs of e (bit q = pair q), 1 < RM <= 64 only
+  int start;      // sorted runs: the run's first index into sorted
 };
 
 template <int RM>
 __device__ __forceinline__ MoeRun moe_run(const MoeArgs& g, const int p) {
   MoeRun r;
-  r.e = __builtin_amdgcn_readfirstlane(g.ids[p]);
   r.rows = 0;
   r.mask = 0;
+  r.start = 0;
+  if constexpr (RM == kMoeSorted) {  // p is a run index
+    r.e = -1;
+    if (p >= __builtin_amdgcn_readfirstlane(*g.nruns)) return r;
+    r.e = __builtin_amdgcn_readfirstlane(g.runs[4 * p]);
+    r.start = __builtin_amdgcn_readfirstlane(g.runs[4 * p + 1]);
+    r.rows = __builtin_amdgcn_readfirstlane(g.runs[4 * p + 2]);
+    return r;
+  }
+  r.e = __builtin_amdgcn_readfirstlane(g.ids[p]);
   if (r.e < 0 || r.e >= g.E) return r;
   if constexpr (RM == 1) {
     r.rows = 1;
@@ -385,8 +405,10 @@ __device__ __forceinline__ MoeRun moe_run(const MoeArgs& g, const int p) {
 
 // pair of row m (< rows) of a run
 template <int RM>
-__device__ __forceinline__ int moe_pair(const MoeRun& r, const int p, int m) {
-  if constexpr (RM == 1) {
+__device__ __forceinline__ int moe_pair(const MoeArgs& g, const MoeRun& r, const int p, int m) {
+  if constexpr (RM == kMoeSorted) {
+    return g.sorted[r.start + m];
+  } else if constexpr (RM == 1) {
     return p;
   } else {
     uint64_t b = r.mask;
@@ -397,14 +419,14 @@ __device__ __forceinline__ int moe_pair(const MoeRun& r, const int p, int m) {
 
 // per-lane x row offsets (elements) of the lane's XCH chunks: row m = chunk / (16 U)
 template <int BITS, int XCH, int RM>
-__device__ __forceinline__ void moe_xrows(const MoeRun& r, const int p, const int div, const int K, const int rows,
-                                          int (&xo)[XCH]) {
+__device__ __forceinline__ void moe_xrows(const MoeArgs& g, const MoeRun& r, const int p, const int div, const int K,
+                                          const int rows, int (&xo)[XCH]) {
   constexpr int U = Geo<BITS>::U;
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int q = 0; q < XCH; ++q) {
     const int m = (lane + 64 * q) / (16 * U);
-    xo[q] = m < rows ? (moe_pair<RM>(r, p, m) / div) * K : 0;
+    xo[q] = m < rows ? (moe_pair<RM>(g, r, p, m) / div) * K : 0;
   }
 }
 
@@ -445,7 +467,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_gate_up(const MoeArgs g) {
   a.w = g.base.w + (size_t)r.e * g.w_stride;
   a.meta = g.base.meta + (size_t)r.e * g.meta_stride;
   int xo[XCH];
-  moe_xrows<BITS, XCH, RM>(r, p, g.topk, a.K, r.rows, xo);
+  moe_xrows<BITS, XCH, RM>(g, r, p, g.topk, a.K, r.rows, xo);
   const int nt[2] = {j, g.ntiles + j};
   oc_f4 yacc[2];
   gemv_accum<BITS, 2, CS, D, W, XCH, BF16>(a, nt, 0, a.NU, r.rows, [&](int q, int) { return a.x + xo[q]; },
@@ -476,7 +498,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_gate_up(const MoeArgs g) {
       uv += BF16 ? oc_bf2f(b[g.I + i]) : oc_h2f(b[g.I + i]);
     }
     const float h = moe_act<BF16>(oc_round_act(gv, BF16), oc_round_act(uv, BF16), g.act, g.alpha, g.limit);
-    g.out[(size_t)moe_pair<RM>(r, p, m) * g.I + i] = BF16 ? oc_f2bf(h) : oc_f2h(h);
+    g.out[(size_t)moe_pair<RM>(g, r, p, m) * g.I + i] = BF16 ? oc_f2bf(h) : oc_f2h(h);
   }
 }
 
@@ -491,7 +513,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_down(const MoeArgs g) {
   a.w = g.base.w + (size_t)r.e * g.w_stride;
   a.meta = g.base.meta + (size_t)r.e * g.meta_stride;
   int xo[XCH];
-  moe_xrows<BITS, XCH, RM>(r, p, 1, a.K, r.rows, xo);
+  moe_xrows<BITS, XCH, RM>(g, r, p, 1, a.K, r.rows, xo);
   const int nt[1] = {j};
   oc_f4 yacc[1];
   gemv_accum<BITS, 1, CS, D, W, XCH, BF16>(a, nt, 0, a.NU, r.rows, [&](int q, int) { return a.x + xo[q]; },
@@ -509,7 +531,70 @@ __global__ __launch_bounds__(64 * W) void k_moe_down(const MoeArgs g) {
     float v = 0.f;
 #pragma unroll
     for (int ww = 0; ww < W; ++ww) v += red[ww * 256 + el];
-    g.part[(size_t)moe_pair<RM>(r, p, m) * a.N_pad + 16 * j + (ln & 15)] = v;
+    g.part[(size_t)moe_pair<RM>(g, r, p, m) * a.N_pad + 16 * j + (ln & 15)] = v;
+  }
+}
+
+// The pairs of each expert in expert order (atomic order within an expert: the
+// rows of an MFMA do not mix, so the outputs do not depend on it), cut into
+// runs of at most 16: runs[r] = {expert, first index into sorted, rows, 0};
+// *nruns = the number of runs.  One workgroup; E <= kMoeMaxE.
+__global__ __launch_bounds__(1024) void k_moe_sort(const int32_t* __restrict__ ids, int pairs, int E,
+                                                   int* __restrict__ sorted, int* __restrict__ runs,
+                                                   int* __restrict__ nruns) {
+  __shared__ int cnt[kMoeMaxE], off[kMoeMaxE], roff[kMoeMaxE];
+  __shared__ int part[2][1024];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < pairs; p += 1024) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  // exclusive scans of the pair counts and run counts: per-thread chunks of experts, then a
+  // scan over the 1024 chunk sums
+  const int per = (E + 1023) / 1024, e0 = min(E, tid * per), e1 = min(E, e0 + per);
+  int s1 = 0, s2 = 0;
+  for (int e = e0; e < e1; ++e) {
+    s1 += cnt[e];
+    s2 += (cnt[e] + 15) / 16;
+  }
+  part[0][tid] = s1;
+  part[1][tid] = s2;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int a1 = tid >= o ? part[0][tid - o] : 0, a2 = tid >= o ? part[1][tid - o] : 0;
+    __syncthreads();
+    part[0][tid] += a1;
+    part[1][tid] += a2;
+    __syncthreads();
+  }
+  int b1 = part[0][tid] - s1, b2 = part[1][tid] - s2;
+  for (int e = e0; e < e1; ++e) {
+    off[e] = b1;
+    roff[e] = b2;
+    b1 += cnt[e];
+    b2 += (cnt[e] + 15) / 16;
+  }
+  if (tid == 1023) *nruns = part[1][1023];
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) {
+    const int c = cnt[e];
+    for (int i = 0; 16 * i < c; ++i) {
+      int* run = runs + 4 * (roff[e] + i);
+      run[0] = e;
+      run[1] = off[e] + 16 * i;
+      run[2] = min(16, c - 16 * i);
+      run[3] = 0;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;  // now the fill cursor of each expert
+  __syncthreads();
+  for (int p = tid; p < pairs; p += 1024) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) sorted[off[e] + atomicAdd(&cnt[e], 1)] = p;
   }
 }
 
@@ -1588,7 +1673,7 @@ namespace {
 
 template <int BITS, int RM>
 struct MoeXch {  // x chunks per lane for RM rows of a unit
-  static constexpr int xc = (RM * 16 * Geo<BITS>::U + 63) / 64;
+  static constexpr int xc = (moe_cap(RM) * 16 * Geo<BITS>::U + 63) / 64;
   static constexpr int X = xc <= 1 ? 1 : (xc <= 4 ? 4 : (xc <= 8 ? 8 : 16));
 };
 
@@ -1599,7 +1684,7 @@ struct MoeD {  // units in flight per wave
 };
 
 struct MoePlan {
-  size_t h_off, part_off, bytes;
+  size_t h_off, part_off, sorted_off, runs_off, nruns_off, bytes;
   int rm, w1, w2;
   size_t lds1, lds2;
 };
@@ -1610,24 +1695,29 @@ MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
   const int h_pad = (H + 15) / 16 * 16;
   p.h_off = 0;
   p.part_off = align256(pairs * I * 2);
-  p.bytes = p.part_off + align256(pairs * h_pad * 4);
+  p.sorted_off = p.part_off + align256(pairs * h_pad * 4);
+  p.runs_off = p.sorted_off + align256(pairs * 4);
+  p.nruns_off = p.runs_off + align256(pairs * 16);
+  p.bytes = p.nruns_off + 256;
   // rows per run: one for a single token (its slots name distinct experts); else 4, or 16
-  // when the pairs spread over the experts give more than 4 per expert on average
-  int rm = env_int("OC_MOE_RM", 0);
+  // when the pairs spread over the experts give more than 4 per expert on average; beyond
+  // 64 pairs, sorted runs of up to 16 (OC_MOE_RM=1: one row per pair)
+  const int rm_env = env_int("OC_MOE_RM", 0);
+  int rm = rm_env;
   if (rm != 1 && rm != 4 && rm != 16) {
     const size_t busy = pairs < (size_t)E ? pairs : (size_t)E;
     rm = M == 1 ? 1 : ((pairs + busy - 1) / busy <= 4 ? 4 : 16);
   }
-  if (pairs > 64) rm = 1;
+  if (pairs > 64) rm = (rm_env == 1 || E > kMoeMaxE) ? 1 : kMoeSorted;
   p.rm = rm;
   const int U = bits == 2 ? 2 : (bits == 3 ? 4 : 1);
-  const size_t slot = (size_t)rm * (128 * U + 8) * 2;
+  const size_t slot = (size_t)moe_cap(rm) * (128 * U + 8) * 2;
   p.w1 = 4;  // gate|up
   const int nu2 = (I + 128 * U - 1) / (128 * U);
   // down: 8 waves for long k-ranges (runs of 1 or 4 rows, groups of 128 or more)
   int w2 = env_int("OC_MOE_W2", 0);
   if (w2 != 4 && w2 != 8) w2 = nu2 >= 24 ? 8 : 4;
-  if (rm == 16 || gs2 % 128 != 0) w2 = 4;
+  if (rm == 16 || rm == kMoeSorted || gs2 % 128 != 0) w2 = 4;
   p.w2 = w2;
   auto lds = [&](int w, int nt) {
     const size_t xb = slot * w, rb = (size_t)w * nt * 256 * 4;
@@ -1653,7 +1743,8 @@ int launch_moe(const MoeArgs& g, int bits, int cs, int w, int rm, size_t lds, in
     OC_HIP(hipGetLastError());                                                                             \
     return 0;                                                                                              \
   }
-#define OC_MKR(B_, CS_, W_) OC_MK(B_, CS_, W_, 1) OC_MK(B_, CS_, W_, 4) OC_MK(B_, CS_, W_, 16)
+#define OC_MKR(B_, CS_, W_) \
+  OC_MK(B_, CS_, W_, 1) OC_MK(B_, CS_, W_, 4) OC_MK(B_, CS_, W_, 16) OC_MK(B_, CS_, W_, kMoeSorted)
 #define OC_MKB(B_) OC_MKR(B_, 4, 4) OC_MKR(B_, 1, 4)
   OC_MKB(2) OC_MKB(3) OC_MKB(4) OC_MKB(8)
   if constexpr (!UP) {  // longer k-ranges of down: 8 waves
@@ -1708,7 +1799,7 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   const int pairs = M * topk;
   auto fill = [&](GemvArgs& a, const oc::Layout& L, int K, int N, int gs, int G) {
     a = GemvArgs{};
-    a.M = mp.rm;
+    a.M = moe_cap(mp.rm);
     a.K = K;
     a.N = N;
     a.N_pad = L.N_pad;
@@ -1724,6 +1815,20 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   MoeArgs g = {};
   g.ids = ids;
   g.pairs = pairs;
+  // workgroup groups per launch: one per pair, or one per sorted run (at most this many)
+  int groups = pairs;
+  if (mp.rm == kMoeSorted) {
+    int* sorted = (int*)(ws + mp.sorted_off);
+    int* runs = (int*)(ws + mp.runs_off);
+    int* nruns = (int*)(ws + mp.nruns_off);
+    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), 0, st, ids, pairs, E, sorted, runs, nruns);
+    OC_HIP(hipGetLastError());
+    g.sorted = sorted;
+    g.runs = runs;
+    g.nruns = nruns;
+    const int bound = (pairs + 15) / 16 + (E < pairs ? E : pairs);
+    groups = bound < pairs ? bound : pairs;
+  }
   g.topk = topk;
   g.E = E;
   g.I = I;
@@ -1743,8 +1848,8 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   g.w_stride = w13_stride;
   g.meta_stride = meta13_stride;
   const int cs13 = (gs13 % 128) == 0 ? 4 : 1, cs2 = (gs2 % 128) == 0 ? 4 : 1;
-  int rc = bf16 ? launch_moe<true, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, pairs * g.ntiles, st)
-                : launch_moe<false, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, pairs * g.ntiles, st);
+  int rc = bf16 ? launch_moe<true, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, groups * g.ntiles, st)
+                : launch_moe<false, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, groups * g.ntiles, st);
   if (rc) return rc;
   // 2. down per run, fp32 sums per pair
   fill(g.base, L2, I, H, gs2, G2);
@@ -1758,8 +1863,8 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   g.meta_stride = meta2_stride;
   float* part = (float*)(ws + mp.part_off);
   g.part = part;
-  rc = bf16 ? launch_moe<true, false>(g, bits, cs2, mp.w2, mp.rm, mp.lds2, pairs * g.ntiles, st)
-            : launch_moe<false, false>(g, bits, cs2, mp.w2, mp.rm, mp.lds2, pairs * g.ntiles, st);
+  rc = bf16 ? launch_moe<true, false>(g, bits, cs2, mp.w2, mp.rm, mp.lds2, groups * g.ntiles, st)
+            : launch_moe<false, false>(g, bits, cs2, mp.w2, mp.rm, mp.lds2, groups * g.ntiles, st);
   if (rc) return rc;
   // 3. weighted sum over the top-k (+ down bias)
   const dim3 grid((H + 255) / 256, M);

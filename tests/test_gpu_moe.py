@@ -212,3 +212,28 @@ def test_vllm_fused_moe_layer(dev, act, bits):
     want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss" if bias else "silu")
     err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
     assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("bits,act", [(4, "silu"), (3, "gpt_oss"), (2, "silu"), (8, "gelu_pytorch_tanh")])
+def test_moe_sorted_runs_many_tokens(dev, monkeypatch, bits, act):
+    """Beyond 64 pairs the pairs are sorted by expert on the device and served 16 rows per weight
+    read: same output bits as one row per pair (OC_MOE_RM=1), and the oracle's values."""
+    E, H, I, k, gs, m = 8, 256, 128, 4, 128, 300
+    bias = act == "gpt_oss"
+    cases, ref = _build(E, H, I, bits, gs, bias, "fp16", seed=110 + bits)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=19)
+    idx, w = _routing(m, k, E, seed=20)
+    idx[5, 1] = -1
+    idx[7, :] = E  # a token with no valid slot
+    xd, idd, wd = x.to(dev), idx.to(dev), w.to(dev)
+    y = moe.moe_forward(xd, idd, wd, ex, act)
+    monkeypatch.setenv("OC_MOE_RM", "1")
+    y1 = moe.moe_forward(xd, idd, wd, ex, act)
+    assert torch.equal(y, y1)
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref,
+                          "gelu_tanh" if act == "gelu_pytorch_tanh" else act)
+    yn = y.float().cpu().numpy()
+    assert np.all(yn[7] == 0.0)
+    err = float(np.max(np.abs(yn - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
