@@ -1084,8 +1084,10 @@ GemvPlan plan_gemv(const oc::Layout& L, int M, int gs) {
   p.ngroups = (L.NT + p.nt - 1) / p.nt;
   // One workgroup streams the whole K of its columns; few column groups get
   // more waves per workgroup.  Each wave owns an x slot of M x (128U + 8) halfs.
+  // A CU holds one 16-wave workgroup of this kernel (its registers), so more
+  // column groups than CUs take 8 waves: one round of workgroups, not two.
   int w = env_int("OC_GEMV_W", 0);
-  if (w != 4 && w != 8 && w != 16) w = (p.ngroups >= 512 || p.nt == 2) ? 8 : 16;
+  if (w != 4 && w != 8 && w != 16) w = (p.ngroups > oc_device_cus() || p.nt == 2) ? 8 : 16;
   if (p.cs == 1 && w == 16) w = 8;
   if (p.xch > 1 && w == 16) w = 8;
   if (p.xch == 16) w = 4;  // the 16-chunk x ring is built for 4 waves only
@@ -1534,6 +1536,10 @@ GroupPlan plan_group(const oc_gptq_part* parts, int n_parts, int M, int K) {
     if (P.perm) off += align256((size_t)M * K * 2);
   }
   if (g.fused) {
+    // the shards' workgroups together: more than one 16-wave workgroup per CU takes 8 waves
+    int blocks = 0;
+    for (int i = 0; i < n_parts; ++i) blocks += oc::make_layout(parts[i].bits, K, parts[i].N).NT;
+    if (blocks > oc_device_cus() && g.w > 8 && env_int("OC_GEMV_W", 0) == 0) g.w = 8;
     if (g.xch > 1 && g.w > 8) g.w = 8;
     while (g.w > 4 && slot * g.w > kGemvLds) g.w /= 2;
     const size_t xb = slot * g.w, rb = (size_t)g.w * 4 * 64 * 4;
