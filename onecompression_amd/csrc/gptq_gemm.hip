@@ -648,15 +648,28 @@ struct GemvDepth {
 // Several layers that read the same activations (the parts of a fused
 // module, which may differ in bit width) in one launch: workgroup b belongs
 // to part p for block_start[p] <= b < block_start[p + 1] and runs that part's
-// decoder (a uniform branch on its bit width).
+// decoder (a uniform branch on its bit width) over part_nt[p] n-tiles (2 for a
+// part whose n-tiles are at most half the bytes of the widest part's, so the
+// workgroups carry about the same bytes; NTMAX = 2 enables it).
 constexpr int kMaxParts = 4;
 struct GemvGroupArgs {
   GemvArgs part[kMaxParts];
   int block_start[kMaxParts + 1];
+  int part_nt[kMaxParts];
   int n_parts;
 };
 
 template <int NT, int W, int XCH, bool BF16>
+__device__ __forceinline__ void gemv_group_part(const GemvArgs& a, const int b) {
+  switch (a.bits) {
+    case 2: gemv_tile<2, NT, 4, GemvDepth<2, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+    case 3: gemv_tile<3, NT, 4, GemvDepth<3, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+    case 4: gemv_tile<4, NT, 4, GemvDepth<4, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+    default: gemv_tile<8, NT, 4, GemvDepth<8, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+  }
+}
+
+template <int NTMAX, int W, int XCH, bool BF16>
 __global__ __launch_bounds__(64 * W) void k_gemv_group(const GemvGroupArgs g) {
   int p = 0;
 #pragma unroll
@@ -664,12 +677,13 @@ __global__ __launch_bounds__(64 * W) void k_gemv_group(const GemvGroupArgs g) {
     if (q < g.n_parts && (int)blockIdx.x >= g.block_start[q]) p = q;
   const GemvArgs& a = g.part[p];
   const int b = blockIdx.x - g.block_start[p];
-  switch (a.bits) {
-    case 2: gemv_tile<2, NT, 4, GemvDepth<2, NT, XCH>::D, W, XCH, BF16>(a, b); break;
-    case 3: gemv_tile<3, NT, 4, GemvDepth<3, NT, XCH>::D, W, XCH, BF16>(a, b); break;
-    case 4: gemv_tile<4, NT, 4, GemvDepth<4, NT, XCH>::D, W, XCH, BF16>(a, b); break;
-    default: gemv_tile<8, NT, 4, GemvDepth<8, NT, XCH>::D, W, XCH, BF16>(a, b); break;
+  if constexpr (NTMAX == 2) {
+    if (g.part_nt[p] == 2) {
+      gemv_group_part<2, W, XCH, BF16>(a, b);
+      return;
+    }
   }
+  gemv_group_part<1, W, XCH, BF16>(a, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -1507,7 +1521,8 @@ namespace {
 
 struct GroupPlan {
   bool fused;
-  int w, xch;
+  int w, xch, ntmax;
+  int nt[kMaxParts];  // n-tiles per workgroup of each part
   size_t lds;
   size_t perm_off[kMaxParts];  // workspace offset of a part's permuted x
   size_t bytes;
@@ -1536,13 +1551,26 @@ GroupPlan plan_group(const oc_gptq_part* parts, int n_parts, int M, int K) {
     if (P.perm) off += align256((size_t)M * K * 2);
   }
   if (g.fused) {
-    // the shards' workgroups together: more than one 16-wave workgroup per CU takes 8 waves
+    // parts whose n-tiles carry at most half the bytes of the widest part's take two n-tiles
+    // per workgroup (one x chunk per lane only); then 8 waves per workgroup when some part
+    // takes two n-tiles or there are more workgroups than CUs (one 16-wave workgroup per CU)
+    // (q 4-bit | k, v 8-bit at M = 1: 8.3 us with one n-tile and 16 waves, 7.1 with one n-tile
+    // and 8 waves, 6.7 with two and 8)
+    int bmax = 0;
+    for (int i = 0; i < n_parts; ++i) bmax = parts[i].bits > bmax ? parts[i].bits : bmax;
+    g.ntmax = 1;
     int blocks = 0;
-    for (int i = 0; i < n_parts; ++i) blocks += oc::make_layout(parts[i].bits, K, parts[i].N).NT;
-    if (blocks > oc_device_cus() && g.w > 8 && env_int("OC_GEMV_W", 0) == 0) g.w = 8;
+    for (int i = 0; i < n_parts; ++i) {
+      const int NT = oc::make_layout(parts[i].bits, K, parts[i].N).NT;
+      const int nt = (g.xch == 1 && 2 * parts[i].bits <= bmax && NT >= 2 && env_int("OC_GROUP_NT", 2) == 2) ? 2 : 1;
+      g.nt[i] = nt;
+      g.ntmax = nt > g.ntmax ? nt : g.ntmax;
+      blocks += (NT + nt - 1) / nt;
+    }
+    if ((blocks > oc_device_cus() || g.ntmax == 2) && g.w > 8 && env_int("OC_GEMV_W", 0) == 0) g.w = 8;
     if (g.xch > 1 && g.w > 8) g.w = 8;
     while (g.w > 4 && slot * g.w > kGemvLds) g.w /= 2;
-    const size_t xb = slot * g.w, rb = (size_t)g.w * 4 * 64 * 4;
+    const size_t xb = slot * g.w, rb = (size_t)g.w * g.ntmax * 4 * 64 * 4;
     g.lds = ((xb > rb ? xb : rb) + 15) / 16 * 16;
     g.bytes = off;
   } else {  // parts one after the other: they reuse one workspace
@@ -1559,14 +1587,15 @@ GroupPlan plan_group(const oc_gptq_part* parts, int n_parts, int M, int K) {
 
 template <bool BF16>
 int launch_group(const GroupPlan& gp, const GemvGroupArgs& ga, int blocks, hipStream_t st) {
-#define OC_GG(W_, XC_)                                                                                \
-  if (gp.w == W_ && gp.xch == XC_) {                                                                  \
-    hipLaunchKernelGGL((k_gemv_group<1, W_, XC_, BF16>), dim3(blocks), dim3(64 * W_), gp.lds, st, ga); \
-    OC_HIP(hipGetLastError());                                                                        \
-    return 0;                                                                                         \
+#define OC_GG(NT_, W_, XC_)                                                                             \
+  if (gp.ntmax == NT_ && gp.w == W_ && gp.xch == XC_) {                                                 \
+    hipLaunchKernelGGL((k_gemv_group<NT_, W_, XC_, BF16>), dim3(blocks), dim3(64 * W_), gp.lds, st, ga); \
+    OC_HIP(hipGetLastError());                                                                          \
+    return 0;                                                                                           \
   }
-  OC_GG(16, 1) OC_GG(8, 1) OC_GG(8, 4) OC_GG(8, 8) OC_GG(8, 16)
-  OC_GG(4, 1) OC_GG(4, 4) OC_GG(4, 8) OC_GG(4, 16)
+  OC_GG(1, 16, 1) OC_GG(1, 8, 1) OC_GG(1, 8, 4) OC_GG(1, 8, 8) OC_GG(1, 8, 16)
+  OC_GG(1, 4, 1) OC_GG(1, 4, 4) OC_GG(1, 4, 8) OC_GG(1, 4, 16)
+  OC_GG(2, 16, 1) OC_GG(2, 8, 1) OC_GG(2, 4, 1)
 #undef OC_GG
   return oc::set_error(OC_ERR_UNSUPPORTED, "no grouped gemv kernel for w=%d xch=%d", gp.w, gp.xch);
 }
@@ -1658,7 +1687,8 @@ extern "C" int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_p
     a.bits = P.bits;
     a.out_f32 = 0;
     ga.block_start[i] = blocks;
-    blocks += L.NT;
+    ga.part_nt[i] = gp.nt[i];
+    blocks += (L.NT + gp.nt[i] - 1) / gp.nt[i];
   }
   for (int i = n_parts; i <= kMaxParts; ++i) ga.block_start[i] = blocks;
   ga.n_parts = n_parts;
