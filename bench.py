@@ -178,8 +178,8 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
 RIDGE_FLOP_PER_BYTE = MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
 # MoE blocks with GPTQ experts (not a BASELINE config): name, hidden, intermediate, experts, top-k, Ms
-MOE_SHAPES = [("Qwen3-30B-A3B experts", 2048, 768, 128, 8, (1, 8, 256)),
-              ("Mixtral-8x7B experts", 4096, 14336, 8, 2, (1, 4, 64))]
+MOE_SHAPES = [("Qwen3-30B-A3B experts", 2048, 768, 128, 8, (1, 8, 256, 2048)),
+              ("Mixtral-8x7B experts", 4096, 14336, 8, 2, (1, 4, 64, 512))]
 
 
 def report_moe(dev, bits=4, gs=128, routings=16):
@@ -217,14 +217,16 @@ def report_moe(dev, bits=4, gs=128, routings=16):
                 w = torch.softmax(torch.randn(m, k, generator=gen), dim=-1)
                 rts.append((idx.to(dev), w.to(dev), len(set(idx.flatten().tolist()))))
             n_rot = routings * copies
+            iters = 2 * n_rot if m <= 64 else 16  # prefill calls hold a large workspace each
             us = _time_graph(lambda i: moe.moe_forward(x, rts[i % routings][0], rts[i % routings][1],
-                                                       exs[(i // routings) % copies]), n_rot, 2 * n_rot)
+                                                       exs[(i // routings) % copies]), n_rot, iters)
             distinct = sum(r[2] for r in rts) / routings
             io = 4 * m * H
             out.append({"block": name, "H": H, "I": I, "E": E, "topk": k, "bits": bits, "gs": gs, "M": m,
                         "dtype": "fp16", "us": round(us, 2), "experts_hit": round(distinct, 2),
                         "GBps": round((distinct * e_bytes + io) / (us * 1e-6) / 1e9, 1),
                         "pair_GBps": round((m * k * e_bytes + io) / (us * 1e-6) / 1e9, 1),
+                        "TFLOPs": round(2.0 * m * k * 3 * H * I / (us * 1e-6) / 1e12, 2),
                         "frac_hbm_peak": round((distinct * e_bytes + io) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         del exs
         torch.cuda.empty_cache()

@@ -156,7 +156,9 @@ size_t oc_moe_workspace_bytes(int M, int H, int I, int topk);
  * Three launches on `stream` (gate|up with the activation, down, the top-k sum), no host
  * synchronisation, no allocation.  Pairs that share an expert share one read of its weights,
  * up to 16 at a time; beyond 64 pairs a fourth launch first sorts the pairs by expert
- * (E <= 2048; above that every pair reads its expert).
+ * (E <= 2048; above that every pair reads its expert).  With at least 32 pairs per expert on
+ * average (prefill) the experts run on the grouped large-M GEMM instead: sort, gather, gate|up,
+ * activation, down, top-k sum (six launches).
  * Replaces _UnfusedExperts.forward, onecomp/utils/unfuse_moe.py:61-114 (with the gpt-oss combine
  * of :380-387) over GPTQ experts, and the WNA16 fused-experts dispatch of
  * vllm_plugins/gptq/vllm_plugin.py:240-283. */

@@ -30,6 +30,13 @@ struct GemmArgs {
   int poff;      // this launch's first partial slot inside a tile
   int tiles_main;  // workgroups below this index compute a whole tile
   int S, kper;     // the remaining tiles are split into S pieces of kper k-blocks
+  // grouped launches (MoE experts, rows sorted by expert): workgroup L computes row tile
+  // L / NB, column block L % NB; gtab[4 i ..] = expert, first row, rows of row tile i
+  // (*gcount tiles); expert e's words / scale-zero words / bias start e * the strides in
+  const int* gtab;
+  const int* gcount;
+  size_t gw_stride, gmeta_stride;
+  int gbias_stride;
 };
 
 // Tile order: consecutive workgroups go to consecutive XCDs; with 8 | MB the
@@ -166,7 +173,7 @@ struct GemmLoads {
   static constexpr int n = 4 * per + (BITS == 1 ? 0 : 2 * (4 / CS));
 };
 
-template <int BITS, int CS, bool BF16, int MT = 4>
+template <int BITS, int CS, bool BF16, int MT = 4, bool GROUPED = false>
 __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   using TL = GemmTile<MT>;
   constexpr int NI = TL::NI;
@@ -177,14 +184,31 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   const int h = lane >> 5, r16 = lane & 15;
   const int L = blockIdx.x;
   // whole tile, or piece `split` of a tile cut along K
-  const bool piece = L >= a.tiles_main;
+  const bool piece = !GROUPED && L >= a.tiles_main;
   const int pidx = L - a.tiles_main;
   const int tile = piece ? a.tiles_main + pidx / a.S : L;
   const int kb0 = piece ? (pidx % a.S) * a.kper : 0;
   const int kb1 = piece ? min(kb0 + a.kper, a.NKB) : a.NKB;
-  int mb, nb;
-  gemm_tile(tile, a.MB, a.NB, mb, nb);
-  const int m0 = mb * TL::BM;
+  int mb, nb, m0, mlim;
+  const uint8_t* wsrc = a.w;
+  const uint32_t* msrc = a.meta;
+  const uint16_t* bsrc = a.bias;
+  if constexpr (GROUPED) {
+    const int i = L / a.NB;
+    nb = L - i * a.NB;
+    if (i >= __builtin_amdgcn_readfirstlane(*a.gcount)) return;
+    const int e = __builtin_amdgcn_readfirstlane(a.gtab[4 * i]);
+    m0 = __builtin_amdgcn_readfirstlane(a.gtab[4 * i + 1]);
+    mlim = m0 + __builtin_amdgcn_readfirstlane(a.gtab[4 * i + 2]);
+    wsrc += (size_t)e * a.gw_stride;
+    msrc += (size_t)e * a.gmeta_stride;
+    if (bsrc) bsrc += (size_t)e * a.gbias_stride;
+    mb = 0;
+  } else {
+    gemm_tile(tile, a.MB, a.NB, mb, nb);
+    m0 = mb * TL::BM;
+    mlim = a.M;
+  }
   const int n0 = nb * kGemmBN + wave * 64;  // first column of this wave
   int nt[2], cl[2];
 #pragma unroll
@@ -200,7 +224,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 
   // x tile loader: wave w, instruction j fills LDS bytes [(XJ w + j) KB, +1 KB):
   // row 16 MT w + 4j + lane/16, chunk position lane % 16.
-  const int rows_here = min(a.M - m0, TL::BM);
+  const int rows_here = min(mlim - m0, TL::BM);
   const int X2 = a.ldx * 2;  // bytes per x row
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (size_t)m0 * a.ldx), 0, rows_here * X2, 0x00020000);
@@ -235,11 +259,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
         const int su = kb >> a.uk_shift, skb = kb & ((1 << a.uk_shift) - 1);
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2)
-          wb[T][q2][0] = *((const uint32_t*)a.w + ((((size_t)nt[T] * a.NU + su) * 64 + cl[q2]) << a.uk_shift) + skb);
+          wb[T][q2][0] = *((const uint32_t*)wsrc + ((((size_t)nt[T] * a.NU + su) * 64 + cl[q2]) << a.uk_shift) + skb);
       } else {
 #pragma unroll
       for (int q2 = 0; q2 < 2; ++q2) {
-        const uint8_t* base = a.w + ((size_t)(nt[T] * a.NU + u) * GG::P) * 1024 + cl[q2] * 16;
+        const uint8_t* base = wsrc + ((size_t)(nt[T] * a.NU + u) * GG::P) * 1024 + cl[q2] * 16;
         uint32_t* o = wb[T][q2];
         if constexpr (BITS == 4 || BITS == 8) {
 #pragma unroll
@@ -267,7 +291,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
       for (int q = 0; q < SPK; ++q) {
         const int k = kb * 128 + 32 * CS * q;
         const int g = min(a.gshift >= 0 ? (k >> a.gshift) : k / a.gs, a.G - 1);
-        mw[T][q] = a.meta[(size_t)g * a.N_pad + nt[T] * 16 + r16];
+        mw[T][q] = msrc[(size_t)g * a.N_pad + nt[T] * 16 + r16];
       }
       }
     }
@@ -407,13 +431,13 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     const int n = n0 + 32 * T + (lane & 31);
     if (n >= a.N) continue;
     float b = 0.f;
-    if (a.bias) b = BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
+    if (bsrc) b = BF16 ? oc_bf2f(bsrc[n]) : oc_h2f(bsrc[n]);
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m < a.M) {
+        if (m < mlim) {
           const float v = fmaf(acc[i][T][r], ps[T], b);
           a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(v) : oc_f2h(v);
         }

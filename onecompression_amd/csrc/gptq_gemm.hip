@@ -537,11 +537,12 @@ __global__ __launch_bounds__(64 * W) void k_moe_down(const MoeArgs g) {
 
 // The pairs of each expert in expert order (atomic order within an expert: the
 // rows of an MFMA do not mix, so the outputs do not depend on it), cut into
-// runs of at most 16: runs[r] = {expert, first index into sorted, rows, 0};
-// *nruns = the number of runs.  One workgroup; E <= kMoeMaxE.
-__global__ __launch_bounds__(1024) void k_moe_sort(const int32_t* __restrict__ ids, int pairs, int E,
-                                                   int* __restrict__ sorted, int* __restrict__ runs,
-                                                   int* __restrict__ nruns) {
+// runs of at most rs: runs[r] = {expert, first index into sorted, rows, 0};
+// counts = {runs, valid pairs}; pos[p] = the index of pair p in sorted (when
+// pos is not null).  One workgroup; E <= kMoeMaxE.
+__global__ __launch_bounds__(1024) void k_moe_sort(const int32_t* __restrict__ ids, int pairs, int E, int rs,
+                                                   int* __restrict__ sorted, int* __restrict__ pos,
+                                                   int* __restrict__ runs, int* __restrict__ counts) {
   __shared__ int cnt[kMoeMaxE], off[kMoeMaxE], roff[kMoeMaxE];
   __shared__ int part[2][1024];
   const int tid = threadIdx.x;
@@ -558,7 +559,7 @@ __global__ __launch_bounds__(1024) void k_moe_sort(const int32_t* __restrict__ i
   int s1 = 0, s2 = 0;
   for (int e = e0; e < e1; ++e) {
     s1 += cnt[e];
-    s2 += (cnt[e] + 15) / 16;
+    s2 += (cnt[e] + rs - 1) / rs;
   }
   part[0][tid] = s1;
   part[1][tid] = s2;
@@ -575,17 +576,20 @@ __global__ __launch_bounds__(1024) void k_moe_sort(const int32_t* __restrict__ i
     off[e] = b1;
     roff[e] = b2;
     b1 += cnt[e];
-    b2 += (cnt[e] + 15) / 16;
+    b2 += (cnt[e] + rs - 1) / rs;
   }
-  if (tid == 1023) *nruns = part[1][1023];
+  if (tid == 1023) {
+    counts[0] = part[1][1023];
+    counts[1] = part[0][1023];
+  }
   __syncthreads();
   for (int e = tid; e < E; e += 1024) {
     const int c = cnt[e];
-    for (int i = 0; 16 * i < c; ++i) {
+    for (int i = 0; rs * i < c; ++i) {
       int* run = runs + 4 * (roff[e] + i);
       run[0] = e;
-      run[1] = off[e] + 16 * i;
-      run[2] = min(16, c - 16 * i);
+      run[1] = off[e] + rs * i;
+      run[2] = min(rs, c - rs * i);
       run[3] = 0;
     }
   }
@@ -594,8 +598,56 @@ __global__ __launch_bounds__(1024) void k_moe_sort(const int32_t* __restrict__ i
   __syncthreads();
   for (int p = tid; p < pairs; p += 1024) {
     const int e = ids[p];
-    if (e >= 0 && e < E) sorted[off[e] + atomicAdd(&cnt[e], 1)] = p;
+    if (e >= 0 && e < E) {
+      const int i = off[e] + atomicAdd(&cnt[e], 1);
+      sorted[i] = p;
+      if (pos) pos[p] = i;
+    }
   }
+}
+
+// Prefill path (rows sorted by expert, large-M GEMM per run of rows): x rows in sorted order.
+__global__ __launch_bounds__(256) void k_moe_gather_x(const uint16_t* __restrict__ x, int H, int topk,
+                                                      const int* __restrict__ sorted,
+                                                      const int* __restrict__ counts, uint16_t* __restrict__ xs) {
+  const int i = blockIdx.x;
+  if (i >= counts[1]) return;
+  const uint16_t* src = x + (size_t)(sorted[i] / topk) * H;
+  for (int c = threadIdx.x; c < H / 8; c += 256)
+    *(oc_u4*)(xs + (size_t)i * H + 8 * c) = *(const oc_u4*)(src + 8 * c);
+}
+
+// Prefill path: h = act(gate, up) for the sorted rows (gate|up rounded, bias included).
+template <bool BF16>
+__global__ void k_moe_act_sorted(const uint16_t* __restrict__ h13, int I, const int* __restrict__ counts, int act,
+                                 float alpha, float limit, uint16_t* __restrict__ h) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = blockIdx.y;
+  if (j >= I || i >= counts[1]) return;
+  const uint16_t* r = h13 + (size_t)i * 2 * I;
+  const float g = BF16 ? oc_bf2f(r[j]) : oc_h2f(r[j]);
+  const float u = BF16 ? oc_bf2f(r[I + j]) : oc_h2f(r[I + j]);
+  const float v = moe_act<BF16>(g, u, act, alpha, limit);
+  h[(size_t)i * I + j] = BF16 ? oc_f2bf(v) : oc_f2h(v);
+}
+
+// Prefill path: y[t] = sum over t's valid slots, in slot order, of w[p] * ys[pos[p]] (the
+// down outputs, rounded with their bias); zero for a token with no valid slot.
+template <bool BF16>
+__global__ void k_moe_combine_sorted(const uint16_t* __restrict__ ys, int H, int topk, int M,
+                                     const int32_t* __restrict__ ids, int E, const float* __restrict__ w,
+                                     const int* __restrict__ pos, uint16_t* __restrict__ y) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (n >= H || t >= M) return;
+  float acc = 0.f;
+  for (int s = 0; s < topk; ++s) {
+    const int p = t * topk + s, e = ids[p];
+    if (e < 0 || e >= E) continue;
+    const uint16_t v = ys[(size_t)pos[p] * H + n];
+    acc = fmaf(w[p], BF16 ? oc_bf2f(v) : oc_h2f(v), acc);
+  }
+  y[(size_t)t * H + n] = BF16 ? oc_f2bf(acc) : oc_f2h(acc);
 }
 
 // y[t] = sum over t's valid slots, in slot order, of w[p] * (part[p] + b2_e); zero for a token
@@ -1721,6 +1773,7 @@ struct MoeD {  // units in flight per wave
 
 struct MoePlan {
   size_t h_off, part_off, sorted_off, runs_off, nruns_off, bytes;
+  size_t g_sorted, g_pos, g_runs, g_counts, g_xs, g_h13, g_h, g_ys;
   int rm, w1, w2;
   size_t lds1, lds2;
 };
@@ -1735,6 +1788,18 @@ MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
   p.runs_off = p.sorted_off + align256(pairs * 4);
   p.nruns_off = p.runs_off + align256(pairs * 16);
   p.bytes = p.nruns_off + 256;
+  // prefill path (its buffers reuse the workspace from 0): sorted, pos, runs, counts, then
+  // x, gate|up, h and the down outputs in sorted row order
+  p.g_sorted = 0;
+  p.g_pos = align256(pairs * 4);
+  p.g_runs = p.g_pos + align256(pairs * 4);
+  p.g_counts = p.g_runs + align256(pairs * 16);
+  p.g_xs = p.g_counts + 256;
+  p.g_h13 = p.g_xs + align256(pairs * H * 2);
+  p.g_h = p.g_h13 + align256(pairs * 2 * I * 2);
+  p.g_ys = p.g_h + align256(pairs * I * 2);
+  const size_t gbytes = p.g_ys + align256(pairs * H * 2);
+  if (pairs >= 32 && gbytes > p.bytes) p.bytes = gbytes;
   // rows per run: one for a single token (its slots name distinct experts); else 4, or 16
   // when the pairs spread over the experts give more than 4 per expert on average; beyond
   // 64 pairs, sorted runs of up to 16 (OC_MOE_RM=1: one row per pair)
@@ -1794,6 +1859,116 @@ int launch_moe(const MoeArgs& g, int bits, int cs, int w, int rm, size_t lds, in
   return oc::set_error(OC_ERR_UNSUPPORTED, "no MoE kernel for bits=%d cs=%d w=%d rows=%d", bits, cs, w, rm);
 }
 
+template <bool BF16>
+int launch_grouped_gemm(const GemmArgs& g, int bits, bool cs4, int mt, int grid, hipStream_t st) {
+  const size_t lds = 2 * (size_t)(64 * mt) * 256;
+#define OC_GG2(B_)                                                                                           \
+  if (bits == B_) {                                                                                          \
+    if (!cs4) hipLaunchKernelGGL((k_gemm<B_, 1, BF16, 4, true>), dim3(grid), dim3(256), lds, st, g);        \
+    else if (mt == 1) hipLaunchKernelGGL((k_gemm<B_, 4, BF16, 1, true>), dim3(grid), dim3(256), lds, st, g); \
+    else if (mt == 2) hipLaunchKernelGGL((k_gemm<B_, 4, BF16, 2, true>), dim3(grid), dim3(256), lds, st, g); \
+    else hipLaunchKernelGGL((k_gemm<B_, 4, BF16, 4, true>), dim3(grid), dim3(256), lds, st, g);             \
+    OC_HIP(hipGetLastError());                                                                               \
+    return 0;                                                                                                \
+  }
+  OC_GG2(2) OC_GG2(3) OC_GG2(4) OC_GG2(8)
+#undef OC_GG2
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no grouped GEMM for bits=%d", bits);
+}
+
+// Prefill: the pairs sorted by expert (runs of 64 MT rows), x gathered into that order, the
+// large-M GEMM per run for gate|up (rounded with its bias, as the reference's linears round)
+// and for down, the activation between them, and the top-k sum through each pair's position.
+int moe_prefill(const void* x, int M, int H, int I, int E, int topk, const int32_t* ids, const float* weights,
+                const void* w13, size_t w13_stride, const uint32_t* meta13, size_t meta13_stride, const void* b13,
+                const void* w2, size_t w2_stride, const uint32_t* meta2, size_t meta2_stride, const void* b2,
+                int bits, int gs13, int gs2, int act, float alpha, float limit, bool bf16, void* y, uint8_t* ws,
+                const MoePlan& mp, hipStream_t st) {
+  const int pairs = M * topk;
+  const int busy = E < pairs ? E : pairs;
+  const int avg = pairs / busy;
+  const bool cs4a = gs13 % 128 == 0, cs4b = gs2 % 128 == 0;
+  int mt = avg >= 256 ? 4 : (avg >= 128 ? 2 : 1);
+  const int mt_env = env_int("OC_MOE_GEMM_MT", 0);
+  if (mt_env == 1 || mt_env == 2 || mt_env == 4) mt = mt_env;
+  if (!cs4a || !cs4b) mt = 4;  // the GEMM for groups below 128 is built for 256-row tiles
+  const int BM = 64 * mt;
+  int* sorted = (int*)(ws + mp.g_sorted);
+  int* pos = (int*)(ws + mp.g_pos);
+  int* runs = (int*)(ws + mp.g_runs);
+  int* counts = (int*)(ws + mp.g_counts);
+  uint16_t* xs = (uint16_t*)(ws + mp.g_xs);
+  uint16_t* h13 = (uint16_t*)(ws + mp.g_h13);
+  uint16_t* h = (uint16_t*)(ws + mp.g_h);
+  uint16_t* ys = (uint16_t*)(ws + mp.g_ys);
+  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), 0, st, ids, pairs, E, BM, sorted, pos, runs, counts);
+  hipLaunchKernelGGL(k_moe_gather_x, dim3(pairs), dim3(256), 0, st, (const uint16_t*)x, H, topk, sorted, counts, xs);
+  OC_HIP(hipGetLastError());
+  const int bound = (pairs + BM - 1) / BM + busy;
+  const int tiles = bound < pairs ? bound : pairs;
+  auto fill = [&](GemmArgs& g, const oc::Layout& L, int K, int N, int gs) {
+    g = GemmArgs{};
+    g.M = pairs;
+    g.K = K;
+    g.N = N;
+    g.N_pad = L.N_pad;
+    g.NT_total = L.NT;
+    g.NU = L.NU;
+    g.G = (K + gs - 1) / gs;
+    g.gs = gs;
+    g.gshift = log2_exact(gs);
+    g.NKB = L.K_pad / 128;
+    g.NB = (L.N_pad + kGemmBN - 1) / kGemmBN;
+    g.ldx = K;
+    g.ldy = N;
+    g.pstride = 1;
+    g.S = 1;
+    g.kper = g.NKB;
+    g.tiles_main = 0x7FFFFFFF;
+    g.gtab = runs;
+    g.gcount = counts;
+  };
+  GemmArgs g;
+  const oc::Layout L13 = oc::make_layout(bits, H, 2 * I), L2 = oc::make_layout(bits, I, H);
+  fill(g, L13, H, 2 * I, gs13);
+  g.x = xs;
+  g.w = (const uint8_t*)w13;
+  g.meta = meta13;
+  g.bias = (const uint16_t*)b13;
+  g.y = h13;
+  g.gw_stride = w13_stride;
+  g.gmeta_stride = meta13_stride;
+  g.gbias_stride = 2 * I;
+  int rc = bf16 ? launch_grouped_gemm<true>(g, bits, cs4a, mt, tiles * g.NB, st)
+                : launch_grouped_gemm<false>(g, bits, cs4a, mt, tiles * g.NB, st);
+  if (rc) return rc;
+  const dim3 ga((I + 255) / 256, pairs);
+  if (bf16) hipLaunchKernelGGL(k_moe_act_sorted<true>, ga, dim3(256), 0, st, h13, I, counts, act, alpha, limit, h);
+  else hipLaunchKernelGGL(k_moe_act_sorted<false>, ga, dim3(256), 0, st, h13, I, counts, act, alpha, limit, h);
+  OC_HIP(hipGetLastError());
+  fill(g, L2, I, H, gs2);
+  g.x = h;
+  g.w = (const uint8_t*)w2;
+  g.meta = meta2;
+  g.bias = (const uint16_t*)b2;
+  g.y = ys;
+  g.gw_stride = w2_stride;
+  g.gmeta_stride = meta2_stride;
+  g.gbias_stride = H;
+  rc = bf16 ? launch_grouped_gemm<true>(g, bits, cs4b, mt, tiles * g.NB, st)
+            : launch_grouped_gemm<false>(g, bits, cs4b, mt, tiles * g.NB, st);
+  if (rc) return rc;
+  const dim3 gc((H + 255) / 256, M);
+  if (bf16)
+    hipLaunchKernelGGL(k_moe_combine_sorted<true>, gc, dim3(256), 0, st, ys, H, topk, M, ids, E, weights, pos,
+                       (uint16_t*)y);
+  else
+    hipLaunchKernelGGL(k_moe_combine_sorted<false>, gc, dim3(256), 0, st, ys, H, topk, M, ids, E, weights, pos,
+                       (uint16_t*)y);
+  OC_HIP(hipGetLastError());
+  return 0;
+}
+
 }  // namespace
 
 extern "C" size_t oc_moe_workspace_bytes(int M, int H, int I, int topk) {
@@ -1848,6 +2023,14 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
     a.ups = L.NU;
     a.bits = bits;
   };
+  // prefill sizes (at least 32 rows per expert on average): the large-M GEMM per run of rows
+  {
+    const int busy = E < pairs ? E : pairs;
+    const int gm = env_int("OC_MOE_GEMM", -1);
+    if (E <= kMoeMaxE && pairs >= 32 && (gm == 1 || (gm != 0 && pairs / busy >= 32)))
+      return moe_prefill(x, M, H, I, E, topk, ids, weights, w13, w13_stride, meta13, meta13_stride, b13, w2,
+                         w2_stride, meta2, meta2_stride, b2, bits, gs13, gs2, act, alpha, limit, bf16, y, ws, mp, st);
+  }
   MoeArgs g = {};
   g.ids = ids;
   g.pairs = pairs;
@@ -1857,7 +2040,8 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
     int* sorted = (int*)(ws + mp.sorted_off);
     int* runs = (int*)(ws + mp.runs_off);
     int* nruns = (int*)(ws + mp.nruns_off);
-    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), 0, st, ids, pairs, E, sorted, runs, nruns);
+    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), 0, st, ids, pairs, E, 16, sorted, (int*)nullptr, runs,
+                       nruns);
     OC_HIP(hipGetLastError());
     g.sorted = sorted;
     g.runs = runs;

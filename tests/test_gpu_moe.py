@@ -217,7 +217,9 @@ def test_vllm_fused_moe_layer(dev, act, bits):
 @pytest.mark.parametrize("bits,act", [(4, "silu"), (3, "gpt_oss"), (2, "silu"), (8, "gelu_pytorch_tanh")])
 def test_moe_sorted_runs_many_tokens(dev, monkeypatch, bits, act):
     """Beyond 64 pairs the pairs are sorted by expert on the device and served 16 rows per weight
-    read: same output bits as one row per pair (OC_MOE_RM=1), and the oracle's values."""
+    read (OC_MOE_GEMM=0 keeps this call off the prefill GEMM path): same output bits as one row
+    per pair (OC_MOE_RM=1), and the oracle's values."""
+    monkeypatch.setenv("OC_MOE_GEMM", "0")
     E, H, I, k, gs, m = 8, 256, 128, 4, 128, 300
     bias = act == "gpt_oss"
     cases, ref = _build(E, H, I, bits, gs, bias, "fp16", seed=110 + bits)
@@ -237,3 +239,42 @@ def test_moe_sorted_runs_many_tokens(dev, monkeypatch, bits, act):
     assert np.all(yn[7] == 0.0)
     err = float(np.max(np.abs(yn - want)) / np.max(np.abs(want)))
     assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("bits,act,gs,dt", [(4, "silu", 128, "fp16"), (3, "gpt_oss", 128, "fp16"),
+                                            (2, "gelu_pytorch_tanh", 64, "fp16"), (8, "silu", 128, "bf16")])
+@pytest.mark.parametrize("mt", [0, 1, 2])
+def test_moe_prefill_gemm(dev, monkeypatch, bits, act, gs, dt, mt):
+    """Prefill sizes (>= 32 rows per expert): rows sorted by expert, the large-M GEMM per run of
+    64 MT rows (MT forced for coverage), against the oracle; tokens with an invalid slot and with
+    no valid slot."""
+    if mt:
+        monkeypatch.setenv("OC_MOE_GEMM_MT", str(mt))
+    E, H, I, k, m = 4, 256, 160, 2, 130
+    bias = act == "gpt_oss"
+    cases, ref = _build(E, H, I, bits, gs, bias, dt, seed=130 + bits)
+    ex = _prepare(cases, bits, gs, dev)
+    td = torch.float16 if dt == "fp16" else torch.bfloat16
+    x = synth.activations(m, H, td, seed=21)
+    idx, w = _routing(m, k, E, seed=22)
+    idx[3, 0] = -1
+    idx[4, :] = E
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, act).float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref,
+                          "gelu_tanh" if act == "gelu_pytorch_tanh" else act, dtype=dt)
+    assert np.all(y[4] == 0.0)
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= (2e-2 if dt == "bf16" else 1e-2), err
+
+
+def test_moe_prefill_matches_runs_path(dev, monkeypatch):
+    """The prefill GEMM path and the 16-row run path agree within the bar on the same call."""
+    E, H, I, k, m, bits = 4, 512, 256, 2, 200, 4
+    cases, ref = _build(E, H, I, bits, 128, False, "fp16", seed=140)
+    ex = _prepare(cases, bits, 128, dev)
+    x = synth.activations(m, H, torch.float16, seed=23).to(dev)
+    idx, w = _routing(m, k, E, seed=24)
+    ya = moe.moe_forward(x, idx.to(dev), w.to(dev), ex, "silu").float()
+    monkeypatch.setenv("OC_MOE_GEMM", "0")
+    yb = moe.moe_forward(x, idx.to(dev), w.to(dev), ex, "silu").float()
+    assert float((ya - yb).abs().max() / yb.abs().max()) <= 1e-2
