@@ -313,3 +313,11 @@ def test_gemm_streaming_mid_m_variants(dev, bits, case, monkeypatch):
     else:
         monkeypatch.setenv("OC_GEMM_STREAM", "1")
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=160 + bits), 30, "fp16", bias=True)
+
+
+# The large-M GEMM with K not a multiple of 128: the last k-block's x chunks past K load as zeros
+# through the buffer range check (the padded codes dequantise to -z s, so stale x there would show).
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("k", [160, 288, 800])
+def test_gemm_large_m_k_tail(dev, bits, k):
+    _gemm_check(dev, _case(k, 512, bits, 32 if k % 64 else 64, seed=180 + bits + k), 300, "fp16")
