@@ -415,6 +415,123 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
   }
 }
 
+// Small M: the same transform as products.  Workgroup (row, jt), four waves,
+// stages the row in LDS (all loads in flight at once) and computes outputs
+// j = 16 jt .. 16 jt + 15 of the length-L transforms of all K blocks:
+// U[j][c] = sum_l W[j][l] x[c L + l] with W[j][l] = (-1)^popcount(j & l)
+// formed in registers (16x16x32 MFMA, A = W, B = x from LDS, fp32
+// accumulate), the waves taking every fourth 32-deep l-step and adding their
+// sums in LDS; u = round(U / sqrt(n)) then forms y[i L + j] = sum_c H_K[i][c]
+// u[j][c] (a second MFMA, one more rounding): the rounding points of
+// k_hadamard, with L / 16 workgroups per row instead of one.  Needs L >= 16
+// and y not overlapping x (workgroups of a row read all of it while others
+// store).
+constexpr int kHadMmMaxKT = 9;                      // K <= 144
+constexpr int kHadMmUS = kHadMmMaxKT * 16 + 24;     // LDS row of the u tile (halves)
+constexpr int kHadMmMaxN = 32768;                   // row staged whole in LDS
+// LDS: block c of the row at c (L + 8) halves (the 16-B pad keeps the 16 lanes of a B read, one
+// block each, in different banks), the waves' partial sums, the u tile.
+size_t had_mm_lds(int n, int K) {
+  return (size_t)(n + 8 * K) * 2 + (size_t)4 * ((K + 15) / 16) * 256 * 4 + 16 * kHadMmUS * 2;
+}
+
+template <int KT, bool BF16>
+__global__ __launch_bounds__(256) void k_hadamard_mm(const uint16_t* __restrict__ x, int ld_x, int n, int L, int K,
+                                                      const int8_t* __restrict__ hadk, float scale,
+                                                      uint16_t* __restrict__ y, int ld_y) {
+  extern __shared__ __align__(16) uint16_t xsm[];
+  const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ntile = L >> 4;
+  const int row = blockIdx.x / ntile, jt = blockIdx.x - row * ntile;
+  const uint16_t* xr = x + (size_t)row * ld_x;
+  uint16_t* yr = y + (size_t)row * ld_y;
+  const int G8 = n >> 3, LP = L + 8, lgL = 31 - __builtin_clz(L);
+  float* red = (float*)(xsm + K * LP);                  // [4 waves][KT][4][64]
+  uint16_t* ut = (uint16_t*)(red + 4 * KT * 256);       // [16][US]
+  // stage the row: 8 chunks of 16 B per thread in flight per batch
+  for (int q0 = 0; q0 < G8; q0 += 256 * 8) {
+    oc_u4 v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int q = q0 + t * 256 + tid;
+      if (q < G8) v[t] = *(const oc_u4*)(xr + 8 * q);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int q = q0 + t * 256 + tid;
+      if (q < G8) *(oc_u4*)(xsm + ((8 * q) >> lgL) * LP + ((8 * q) & (L - 1))) = v[t];
+    }
+  }
+  __syncthreads();
+  constexpr int KP = (16 * KT + 31) & ~31;  // c padded to whole 32-deep MFMA steps
+  constexpr int US = KP + 8;
+  const uint32_t one = BF16 ? 0x3F80u : 0x3C00u;
+  const int j = 16 * jt + col;
+  oc_f4 acc[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) acc[t] = oc_f4{0.f, 0.f, 0.f, 0.f};
+  for (int l0 = 32 * wave; l0 < L; l0 += 128) {
+    const int lb = l0 + 8 * kq;  // this lane's 8 l's
+    uint32_t aw[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t s0 = __builtin_popcount(j & (lb + 2 * t)) & 1, s1 = __builtin_popcount(j & (lb + 2 * t + 1)) & 1;
+      aw[t] = (one | (s0 << 15)) | ((one | (s1 << 15)) << 16);
+    }
+    const oc_u4 av = oc_u4{aw[0], aw[1], aw[2], aw[3]};
+#pragma unroll
+    for (int ct = 0; ct < KT; ++ct) {
+      const int c = 16 * ct + col;
+      oc_u4 bv = oc_u4{0u, 0u, 0u, 0u};
+      if (c < K && lb < L) bv = *(const oc_u4*)(xsm + c * LP + lb);
+      acc[ct] = oc_mfma16<BF16>(av, bv, acc[ct]);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < KT; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[((wave * KT + ct) * 4 + r) * 64 + lane] = acc[ct][r];
+  __syncthreads();
+  // the four partial sums; red[(ct * 4 + r) * 64 + lane] = U[j = 16 jt + 4 kq + r][c = 16 ct + col]
+  for (int e = tid; e < KT * 256; e += 256) {
+    const float u = red[e] + red[KT * 256 + e] + red[2 * KT * 256 + e] + red[3 * KT * 256 + e];
+    const int ln = e & 63, r = (e >> 6) & 3, ct = e >> 8;
+    const int jj = 4 * (ln >> 4) + r, c = 16 * ct + (ln & 15);
+    if (K == 1) {
+      if (c == 0) yr[16 * jt + jj] = had_out<BF16>(u * scale);
+    } else {
+      ut[jj * US + c] = had_out<BF16>(u * scale);
+    }
+  }
+  if (K == 1) return;
+  if constexpr (KP > 16 * KT) {  // c in [16 KT, KP): zero
+    for (int q = tid; q < 16 * (KP - 16 * KT); q += 256)
+      ut[(q / (KP - 16 * KT)) * US + 16 * KT + q % (KP - 16 * KT)] = 0;
+  }
+  __syncthreads();
+  // y[i][j] = sum_c u[j][c] H[i][c]: A = u rows j, B = H_K rows i (k = c); wave w takes i-tiles w, w + 4, ...
+  for (int it = wave; it < KT; it += 4) {
+    const int i = 16 * it + col;
+    oc_f4 a2 = oc_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c0 = 0; c0 < KP; c0 += 32) {
+      const int cb = c0 + 8 * kq;
+      const oc_u4 uv = *(const oc_u4*)(ut + col * US + cb);
+      uint32_t p0 = 0, p1 = 0, p2 = 0, p3 = 0;
+      if (i < K && cb < K) had_signs<BF16>(*(const uint32_t*)(hadk + i * K + cb), p0, p1);
+      if (i < K && cb + 4 < K) had_signs<BF16>(*(const uint32_t*)(hadk + i * K + cb + 4), p2, p3);
+      a2 = oc_mfma16<BF16>(uv, oc_u4{p0, p1, p2, p3}, a2);
+    }
+    // a2[r] = y[i = 16 it + col][j = 16 jt + 4 kq + r]
+    if (i < K) {
+      uint16_t* yo = yr + (size_t)i * L + 16 * jt + 4 * kq;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yo[r] = had_out<BF16>(a2[r]);
+    }
+  }
+}
+
 // Dynamic LDS of k_hadamard for (n, K) with chunks of J columns.
 size_t had_lds_bytes(int n, int K, int J) {
   size_t b = (size_t)n * 4;
@@ -432,6 +549,11 @@ int had_chunk_log2(int n, int K) {
 }
 
 }  // namespace
+
+static int env_int_had(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
 
 extern "C" int oc_hadamard_order(int n) { return n > 0 ? pick_order(n) : 0; }
 
@@ -469,6 +591,32 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
   const bool vx = n % 8 == 0 && ld_x % 8 == 0 && ((uintptr_t)x & 15) == 0;
   const bool vy = n % 8 == 0 && ld_y % 8 == 0 && ((uintptr_t)y & 15) == 0;
   const bool vy4 = (n / K) % 4 == 0 && ld_y % 4 == 0 && ((uintptr_t)y & 7) == 0;
+  const int Lh = n / K;
+  const char *xb = (const char*)x, *yb = (const char*)y;
+  const bool overlap = xb < yb + (size_t)M * ld_y * 2 && yb < xb + (size_t)M * ld_x * 2;
+  const int mm_max = env_int_had("OC_HAD_MM_M", 16);
+  if (M <= mm_max && Lh >= 16 && K <= 16 * kHadMmMaxKT && n <= kHadMmMaxN && !overlap && vx &&
+      ((uintptr_t)y & 1) == 0) {
+    hipStream_t st = (hipStream_t)stream;
+    const float sc = 1.0f / sqrtf((float)n);
+    const dim3 grid((unsigned)(M * (Lh / 16)));
+    const size_t mlds = had_mm_lds(n, K);
+    const int KT = (K + 15) / 16;
+    const bool bf = act_dtype == OC_DTYPE_BF16;
+#define OC_HM(KT_)                                                                                              \
+  if (KT == KT_) {                                                                                              \
+    if (bf)                                                                                                     \
+      hipLaunchKernelGGL((k_hadamard_mm<KT_, true>), grid, dim3(256), mlds, st, (const uint16_t*)x, ld_x, n, Lh, K, \
+                         hadk, sc, (uint16_t*)y, ld_y);                                                         \
+    else                                                                                                        \
+      hipLaunchKernelGGL((k_hadamard_mm<KT_, false>), grid, dim3(256), mlds, st, (const uint16_t*)x, ld_x, n, Lh,   \
+                         K, hadk, sc, (uint16_t*)y, ld_y);                                                      \
+  }
+    OC_HM(1) OC_HM(2) OC_HM(3) OC_HM(4) OC_HM(5) OC_HM(6) OC_HM(7) OC_HM(8) OC_HM(9)
+#undef OC_HM
+    OC_HIP(hipGetLastError());
+    return 0;
+  }
   const int per_cu = (int)(kHadMaxLds / lds) < 2 ? 1 : 2;
   const int grid = M < oc_device_cus() * per_cu ? M : oc_device_cus() * per_cu;
   hipStream_t st = (hipStream_t)stream;

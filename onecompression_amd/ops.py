@@ -251,6 +251,14 @@ def hadamard(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tenso
     if out is None:
         out = torch.empty_like(x2)
     blk = hadamard_block(k, x.device)
-    N.call("oc_hadamard", _ptr(x2), x2.shape[0], n, x2.stride(0), _ptr(blk), k, _DT[x.dtype], _ptr(out),
-           out.stride(0), _stream(x.device))
+    # An output overlapping the input is written through a fresh buffer: the library serves
+    # overlapping buffers with its one-workgroup-per-row kernel, whose fp32 summation order
+    # differs from the small-M kernel's, and in-place calls should give the same bits.
+    lo, hi = x2.data_ptr(), x2.data_ptr() + x2.shape[0] * x2.stride(0) * x2.element_size()
+    olo, ohi = out.data_ptr(), out.data_ptr() + out.shape[0] * out.stride(0) * out.element_size()
+    dst = torch.empty_like(x2) if (olo < hi and lo < ohi) else out
+    N.call("oc_hadamard", _ptr(x2), x2.shape[0], n, x2.stride(0), _ptr(blk), k, _DT[x.dtype], _ptr(dst),
+           dst.stride(0), _stream(x.device))
+    if dst is not out:
+        out.copy_(dst)
     return out.reshape(x.shape)
