@@ -7,9 +7,10 @@ Mirrors vllm_plugins/utils/rotation.py:
   transforms the ``mlp.down_proj`` input online, y = (H_K (x) H_L) x / sqrt(n),
   through a forward pre-hook installed at create_weights /
   process_weights_after_loading, as the reference does for tp = 1.  The
-  transform is ``ops.hadamard`` (two HIP launches: the length-L transforms in
+  transform is ``ops.hadamard`` (one HIP launch: the length-L transforms in
   fp32, rounded once to the activation dtype, then the K x K mix on MFMA with
-  fp32 accumulation and one more rounding).  The reference's default
+  fp32 accumulation and one more rounding; up to 16 rows as products over
+  L / 16 workgroups per row, from 32 rows one workgroup per row).  The reference's default
   ``fp32_had=False`` rounds three times (transform, 1/sqrt(n), H_K product);
   ``fp32_had=True`` rounds once, and this result differs from it by the one
   intermediate rounding;
