@@ -1457,7 +1457,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     return launch_reduce(bf16, a.partial, p.S, M, N, L.N_pad, bias, y, ldy, st);
   }
   if (use_gemm(M, L.N_pad, gs)) {
-    GemmArgs g;
+    GemmArgs g = {};
     g.x = xa;
     g.w = (const uint8_t*)packed;
     g.meta = meta;
@@ -1928,7 +1928,7 @@ int moe_prefill(const void* x, int M, int H, int I, int E, int topk, const int32
     g.gtab = runs;
     g.gcount = counts;
   };
-  GemmArgs g;
+  GemmArgs g = {};
   const oc::Layout L13 = oc::make_layout(bits, H, 2 * I), L2 = oc::make_layout(bits, I, H);
   fill(g, L13, H, 2 * I, gs13);
   g.x = xs;
