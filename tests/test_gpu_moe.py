@@ -278,3 +278,18 @@ def test_moe_prefill_matches_runs_path(dev, monkeypatch):
     monkeypatch.setenv("OC_MOE_GEMM", "0")
     yb = moe.moe_forward(x, idx.to(dev), w.to(dev), ex, "silu").float()
     assert float((ya - yb).abs().max() / yb.abs().max()) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [64, 256])
+def test_moe_realistic_expert_shape(dev, m):
+    """Qwen3-MoE-like experts (H 2048, I 768, 16 experts, top-4, 4-bit g128): 16-row sorted runs
+    at M = 64 (16 rows per expert), the prefill GEMM at M = 256 (64 per expert)."""
+    E, H, I, k, gs, bits = 16, 2048, 768, 4, 128, 4
+    cases, ref = _build(E, H, I, bits, gs, False, "fp16", seed=160)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=25)
+    idx, w = _routing(m, k, E, seed=26)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "silu").float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
