@@ -28,9 +28,13 @@ def _rel(y, ref):
 QKV_MIXED = [(4, 256, 128, False), (8, 64, 128, False), (8, 64, 128, False)]   # config-1 style q@4b, k/v@8b
 ALL_BITS = [(2, 96, 128, False), (3, 64, 128, True), (4, 128, 256, False), (8, 32, -1, False)]
 ODD_GROUPS = [(4, 128, 64, False), (8, 64, 128, False)]  # a group of 64: parts one after the other
+# half-width parts (two n-tiles per workgroup at M <= 2) with odd n-tile counts: the last
+# workgroup's second n-tile is past the part
+HALF_ODD = [(4, 272, 128, False), (8, 48, 128, False), (2, 208, 128, False)]
 
 
-@pytest.mark.parametrize("parts", [QKV_MIXED, ALL_BITS, ODD_GROUPS], ids=["qkv", "all_bits", "odd_groups"])
+@pytest.mark.parametrize("parts", [QKV_MIXED, ALL_BITS, ODD_GROUPS, HALF_ODD],
+                         ids=["qkv", "all_bits", "odd_groups", "half_odd"])
 @pytest.mark.parametrize("m", [1, 3, 16, 40])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_grouped_matches_oracle_per_part(dev, parts, m, dtype):
