@@ -293,3 +293,18 @@ def test_moe_realistic_expert_shape(dev, m):
     want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
     err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
     assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("m", [3, 130])
+def test_moe_per_channel_groups(dev, m):
+    """group_size = -1 (one group over K; I = 160 is not a power of two): decode path at M = 3,
+    prefill GEMM at M = 130."""
+    E, H, I, k, bits = 4, 256, 160, 2, 4
+    cases, ref = _build(E, H, I, bits, -1, True, "fp16", seed=170)
+    ex = _prepare(cases, bits, -1, dev)
+    x = synth.activations(m, H, torch.float16, seed=27)
+    idx, w = _routing(m, k, E, seed=28)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, "gpt_oss").float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
