@@ -471,7 +471,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every box in this build has a single MI355X and the "
-              "multi-GPU path is a design (see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "path is not built in this one-GPU build; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
