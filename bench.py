@@ -470,8 +470,8 @@ def main():
                     help="only run a 256 MiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: every box in this build has a single MI355X and the "
-              "path is not built in this one-GPU build; run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only (the multi-GPU path is not part of this build); "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
