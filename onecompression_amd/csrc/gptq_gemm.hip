@@ -759,6 +759,7 @@ struct StreamArgs {
   const uint16_t* bias;
   uint16_t* y;
   int M, K, K_pad, N, N_pad, NT_total, NU, G, gs, gkb_shift, ldy;
+  int tpw;  // k_gemv_stream_bal: n-tiles per workgroup
 };
 
 template <int BITS, int D, int MR, int KS, bool BF16>
@@ -897,6 +898,166 @@ __global__ __launch_bounds__(256, 4) void k_gemv_stream(const StreamArgs a) {
     for (int r = 0; r < MR; ++r) {
       const int m = 4 * kq + r;
       if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(yacc[r] + b) : oc_f2h(yacc[r] + b);
+    }
+  }
+}
+
+// Wide layers whose n-tile count is not a multiple of 4 x CUs, where
+// k_gemv_stream would leave some CUs with twice the n-tiles of others (1792
+// n-tiles on 256 CUs: 192 CUs run 8 waves, 64 run 4): each workgroup of 8
+// waves owns T consecutive n-tiles (one workgroup per CU for T = ceil(n-tiles
+// / CUs)) and splits their T x NU units evenly over its waves, so a wave's
+// range may start or end inside an n-tile.  A range is at most NU units long
+// (T <= 8), so a wave touches at most two n-tiles and keeps one partial sum for
+// each; the partials of an n-tile meet in LDS and are added in wave order.  A
+// wave's unit count is rounded up to a multiple of D with loads of its last
+// unit again (no consume), so every load stays unconditional.
+// ---------------------------------------------------------------------------
+constexpr int kStreamBalWaves = 8;
+
+template <int BITS, int D, int MR, bool BF16>
+__global__ __launch_bounds__(64 * kStreamBalWaves) void k_gemv_stream_bal(const StreamArgs a) {
+  using GG = Geo<BITS>;
+  constexpr int U = GG::U, P = GG::P, WV = kStreamBalWaves;
+  constexpr float OFF = dec_offset<BITS, BF16>();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, kq = lane >> 4;
+  const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<BF16>());
+  const int M = a.M, NU = a.NU, T = a.tpw;
+  const int t0 = blockIdx.x * T;  // first n-tile of the workgroup
+  const int total = T * NU;       // units of the workgroup's n-tiles
+  const int ws = wave * total / WV, we = (wave + 1) * total / WV;
+  const int npad = ((total + WV - 1) / WV + D - 1) / D * D;  // units per wave, incl. repeats
+
+  // LDS: x rows [M][K_pad + 8] (zero past K), group sums [G][16] fp32, then
+  // the partial sums [8 waves][2][MR][64] fp32
+  extern __shared__ __align__(16) uint16_t xl[];
+  const int XL = a.K_pad + 8;
+  float* xsum = (float*)(xl + (size_t)M * XL);
+  const int nkb = a.K_pad / 128;
+  float* red = xsum + nkb * 16;
+  // the workgroup's n-tiles are contiguous in the packed weights
+  const int tiles = min(T, a.NT_total - t0);
+  const __amdgpu_buffer_rsrc_t wr = oc_rsrc(a.w + (size_t)t0 * NU * P * 1024, (uint32_t)tiles * NU * P * 1024);
+  const __amdgpu_buffer_rsrc_t mr = oc_rsrc(a.meta, (uint32_t)a.G * a.N_pad * 4);
+  const uint16_t* arow = xl + min(col, M - 1) * XL + 8 * kq;
+  const float* srow = xsum + 4 * kq;
+  const int first = ws / NU;  // the wave's first n-tile (workgroup-local)
+  uint32_t wb[D][4 * P];
+  uint32_t mb[D][U];
+  auto load = [&](int f, uint32_t (&w)[4 * P], uint32_t (&m)[U]) {
+    f = min(f, we - 1);
+    const int tl = f / NU, uk = f - tl * NU;
+#pragma unroll
+    for (int pt = 0; pt < P; ++pt) {
+      const oc_u4 v = oc_bload16_nt(wr, (uint32_t)(f * P + pt) * 1024 + lane * 16);
+      w[4 * pt] = v[0];
+      w[4 * pt + 1] = v[1];
+      w[4 * pt + 2] = v[2];
+      w[4 * pt + 3] = v[3];
+    }
+    const uint32_t mcol = (uint32_t)(min(t0 + tl, a.NT_total - 1) * 16 + col) * 4;
+#pragma unroll
+    for (int kbl = 0; kbl < U; ++kbl) {
+      const int g = (uk * U + kbl) >> a.gkb_shift;
+      m[kbl] = __builtin_amdgcn_raw_buffer_load_b32(mr, mcol + (uint32_t)(g * a.N_pad) * 4, 0, 0);
+    }
+  };
+  const int cpr = a.K_pad / 8;
+  for (int c = threadIdx.x; c < M * cpr; c += 64 * WV) {
+    const int m = c / cpr, k = 8 * (c % cpr);
+    oc_u4 v = oc_u4{0u, 0u, 0u, 0u};
+    if (k < a.K) v = *(const oc_u4*)(a.x + (size_t)m * a.K + k);
+    *(oc_u4*)(xl + m * XL + k) = v;
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < M * nkb * 16; c += 64 * WV) {
+    const int e = c >> 4, kb = e % nkb, m = e / nkb;
+    const oc_u4 v = *(const oc_u4*)(xl + m * XL + kb * 128 + 8 * (c & 15));
+    float sum = 0.f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const uint32_t pr = v[h];
+      sum += (BF16 ? oc_bf2f((uint16_t)(pr & 0xFFFFu)) : oc_h2f((uint16_t)(pr & 0xFFFFu))) +
+             (BF16 ? oc_bf2f((uint16_t)(pr >> 16)) : oc_h2f((uint16_t)(pr >> 16)));
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+    if ((c & 15) == 0) xsum[kb * 16 + m] = sum;
+  }
+  __syncthreads();
+
+  oc_f4 yacc = oc_f4{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int f, const uint32_t (&w)[4 * P], const uint32_t (&m)[U]) {
+    if (f >= we) return;  // a repeat load past the wave's range
+    const int tl = f / NU, uk = f - tl * NU;
+#pragma unroll
+    for (int kbl = 0; kbl < U; ++kbl) {
+      const int kb = uk * U + kbl;
+      oc_u4 av[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[t] = *(const oc_u4*)(arow + kb * 128 + 32 * t);
+      oc_u4 bq[4];
+      decode_kblock<BITS, BF16>(w, kbl, bq, msk, mag);
+      oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(av[t], bq[t], acc);
+      const uint32_t md = m[kbl];
+      const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
+      const float oz = OFF + (float)(md >> 16);
+      const float* sg = srow + kb * 16;
+      if constexpr (MR == 1) {
+        yacc[0] = fmaf(sc, fmaf(-oz, sg[0], acc[0]), yacc[0]);
+      } else {
+        const oc_f4 xs = *(const oc_f4*)sg;
+#pragma unroll
+        for (int r = 0; r < MR; ++r) yacc[r] = fmaf(sc, fmaf(-oz, xs[r], acc[r]), yacc[r]);
+      }
+    }
+    if (uk == NU - 1 || f == we - 1) {  // the wave leaves this n-tile: park its partial sum
+      const int slot = tl - first;
+#pragma unroll
+      for (int r = 0; r < MR; ++r) red[((wave * 2 + slot) * MR + r) * 64 + lane] = yacc[r];
+      yacc = oc_f4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  if (we > ws) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      load(ws + d, wb[d], mb[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int i0 = 0; i0 < npad - D; i0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        consume(ws + i0 + d, wb[d], mb[d]);
+        load(ws + i0 + D + d, wb[d], mb[d]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) consume(ws + npad - D + d, wb[d], mb[d]);
+  }
+  __syncthreads();
+  // wave w < tiles finishes n-tile t0 + w: the partials of every wave whose
+  // range meets the n-tile's units [w NU, (w + 1) NU), in wave order
+  if (wave >= tiles) return;
+  oc_f4 y = oc_f4{0.f, 0.f, 0.f, 0.f};
+  for (int v = 0; v < WV; ++v) {
+    const int vs = v * total / WV, ve = (v + 1) * total / WV;
+    if (vs >= ve || vs >= (wave + 1) * NU || ve <= wave * NU) continue;
+    const int slot = wave - vs / NU;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) y[r] += red[((v * 2 + slot) * MR + r) * 64 + lane];
+  }
+  const int n = (t0 + wave) * 16 + col;
+  if (n < a.N) {
+    float b = 0.f;
+    if (a.bias != nullptr) b = BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      const int m = 4 * kq + r;
+      if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(y[r] + b) : oc_f2h(y[r] + b);
     }
   }
 }
@@ -1290,9 +1451,45 @@ int stream_depth(const oc::Layout& L, int M, int gs) {
   return d >= 2 && nu >= d ? d : 0;
 }
 
+// n-tiles per workgroup of k_gemv_stream_bal for this layer, or 0 for
+// k_gemv_stream: the balanced kernel takes layers at M >= 3 whose n-tiles
+// would not give every CU the same number of 4-wave workgroups, at T =
+// ceil(n-tiles / CUs) <= 8 (measured: at M = 1 k_gemv_stream is faster on the
+// configs' wide layers even where its CUs are unevenly loaded).
+// OC_GEMV_STREAM_BAL=0 turns it off, =1 forces it where T <= 8.
+int stream_bal_tiles(const oc::Layout& L, int bits, int M, int ks) {
+  const int e = env_int("OC_GEMV_STREAM_BAL", -1);
+  if (e == 0 || ks != 1 || (e != 1 && M < 3)) return 0;
+  const int cus = oc_device_cus();
+  const int t = (L.NT + cus - 1) / cus;
+  const size_t tile_bytes = (size_t)L.NU * (bits == 3 ? 3 : (bits == 8 ? 2 : 1)) * 1024;
+  if (t > kStreamBalWaves || (size_t)t * tile_bytes >= ((size_t)1 << 32)) return 0;
+  if (e != 1 && L.NT % (4 * cus) == 0) return 0;
+  return t;
+}
+
 template <bool BF16>
-int dispatch_stream(int bits, int d, int M, const oc::Layout& L, const StreamArgs& a, hipStream_t st) {
+int dispatch_stream(int bits, int d, int M, const oc::Layout& L, StreamArgs a, hipStream_t st) {
   const int ks = stream_ksplit(L);
+  a.tpw = stream_bal_tiles(L, bits, M, ks);
+  if (a.tpw > 0) {
+    const dim3 grid((L.NT + a.tpw - 1) / a.tpw), block(64 * kStreamBalWaves);
+    const int mr = M >= 3 ? 4 : M;
+    const size_t lds = stream_lds(L, M) + (size_t)kStreamBalWaves * 2 * mr * 64 * 4;
+#define OC_SB(B_, D_, MR_)                                                          \
+  if (bits == B_ && d == D_ && mr == MR_) {                                         \
+    hipLaunchKernelGGL((k_gemv_stream_bal<B_, D_, MR_, BF16>), grid, block, lds, st, a); \
+    OC_HIP(hipGetLastError());                                                      \
+    return 0;                                                                       \
+  }
+#define OC_SBB(B_) OC_SB(B_, 2, 1) OC_SB(B_, 2, 2) OC_SB(B_, 2, 4)
+#define OC_SBB4(B_) OC_SBB(B_) OC_SB(B_, 4, 1) OC_SB(B_, 4, 2) OC_SB(B_, 4, 4)
+    OC_SBB4(2) OC_SBB4(3) OC_SBB4(4) OC_SBB4(8)
+#undef OC_SBB4
+#undef OC_SBB
+#undef OC_SB
+    return oc::set_error(OC_ERR_UNSUPPORTED, "no balanced streaming gemv for bits=%d d=%d", bits, d);
+  }
   const dim3 grid((L.NT * ks + 3) / 4), block(256);
   size_t lds = stream_lds(L, M);
   const int mr = M >= 3 ? 4 : M;
@@ -1390,7 +1587,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
   const bool bf16 = act_dtype == OC_DTYPE_BF16;
   const int sd = M <= kGemvMaxM ? stream_depth(L, M, gs) : 0;
   if (sd == 0 && use_gemm_stream(L, M, gs)) {
-    StreamArgs a;
+    StreamArgs a = {};
     a.x = xa;
     a.w = (const uint8_t*)packed;
     a.meta = meta;
@@ -1411,7 +1608,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
   }
   if (M <= kGemvMaxM) {
     if (sd > 0) {
-      StreamArgs a;
+      StreamArgs a = {};
       a.x = xa;
       a.w = (const uint8_t*)packed;
       a.meta = meta;

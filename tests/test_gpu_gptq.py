@@ -272,6 +272,36 @@ def test_gemm_streaming_variants(dev, bits, case, monkeypatch):
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=95 + bits), 5, "fp16", bias=True)
 
 
+# Layers whose n-tiles do not give every CU the same number of 4-wave workgroups take the
+# balanced streaming GEMV (8 waves share T n-tiles' units evenly, so a wave's range may start or
+# end inside an n-tile; the partial sums of an n-tile meet in LDS).  On 256 CUs these n give
+# T = 1..8 n-tiles per workgroup, a partial last workgroup, and (T = 1 with two units per n-tile)
+# waves with no units at all.
+BAL_SHAPES = [(4096, 28672, 1), (512, 16384 + 32, 3), (1024, 2048 + 32, 4), (512, 1024, 2),
+              (1024, 4096 + 96, 1), (640, 28672 + 32, 2), (256, 9600, 4), (768, 14400, 1),
+              (1152, 22400, 3)]
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("k,n,m", BAL_SHAPES)
+def test_gemm_streaming_balanced(dev, bits, k, n, m, monkeypatch):
+    monkeypatch.setenv("OC_GEMV_STREAM", "1")
+    monkeypatch.setenv("OC_GEMV_STREAM_BAL", "1")
+    _gemm_check(dev, _case(k, n, bits, seed=500 + bits + m), m, "fp16", bias=(m != 1))
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("case", ["act", "bf16", "g256"])
+def test_gemm_streaming_balanced_variants(dev, bits, case, monkeypatch):
+    monkeypatch.setenv("OC_GEMV_STREAM_BAL", "1")
+    if case == "act":
+        _gemm_check(dev, _case(1024, 17408, bits, 128, True, seed=510 + bits), 2, "fp16", bias=True)
+    elif case == "bf16":
+        _gemm_check(dev, _case(512, 17408, bits, seed=520 + bits), 4, "bf16", bias=True)
+    else:
+        _gemm_check(dev, _case(1024, 17408, bits, 256, False, seed=530 + bits), 1, "fp16")
+
+
 # The streaming GEMV folds the zero point in through per-k-block sums of x (an fp32 offset term
 # of 1024 sum(x) that cancels): tiny activations and a wide dynamic range stay within the bar.
 @pytest.mark.parametrize("m", [1, 4])
