@@ -31,6 +31,7 @@ def _replays(dev, make_inputs, run, n=3):
 
 @pytest.mark.parametrize("k,n,bits,m,dt", [
     (4096, 28672, 3, 1, torch.float16),   # streaming GEMV (wide)
+    (4096, 28672, 3, 4, torch.float16),   # balanced streaming GEMV (wide, uneven CU load)
     (4096, 4096, 4, 1, torch.float16),    # k_gemv
     (1024, 16384, 2, 24, torch.float16),  # streaming GEMM (mid M)
     (512, 1024, 8, 40, torch.bfloat16),   # skinny / split-K
