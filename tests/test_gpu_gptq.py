@@ -290,6 +290,14 @@ def test_gemm_streaming_balanced(dev, bits, k, n, m, monkeypatch):
     _gemm_check(dev, _case(k, n, bits, seed=500 + bits + m), m, "fp16", bias=(m != 1))
 
 
+# K = 8192 at M = 4: x and its k-block sums take 70 KB of LDS (86 KB with the balanced kernel's
+# partial sums), above the 64 KB of earlier CDNA parts.
+@pytest.mark.parametrize("bal", ["0", "1"])
+def test_gemm_streaming_large_lds(dev, bal, monkeypatch):
+    monkeypatch.setenv("OC_GEMV_STREAM_BAL", bal)
+    _gemm_check(dev, _case(8192, 16384 + 32, 4, seed=540), 4, "fp16", bias=True)
+
+
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("case", ["act", "bf16", "g256"])
 def test_gemm_streaming_balanced_variants(dev, bits, case, monkeypatch):
