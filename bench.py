@@ -498,7 +498,13 @@ def main():
     r = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev)
     dom = max(r["kernels"], key=lambda k: k["us"])
     value = r["step_bytes"] / r["wall_s"] / 1e9
-    kname = f"k_gemv_stream {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b"
+    # the wide dominant layer's kernel at M <= 4 (k_gemv_stream_bal at M >= 3 when its n-tiles load
+    # the CUs unevenly, as config 1's gate|up does); other M name the call only
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    kern = "dominant call"
+    if args.m <= 4:
+        kern = "k_gemv_stream" if args.m <= 2 or (dom["N"] // 16) % (4 * cus) == 0 else "k_gemv_stream_bal"
+    kname = f"{kern} {dom['name']} {dom['K']}->{dom['N']} {dom['bits']}b"
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
