@@ -290,6 +290,21 @@ def test_gemm_streaming_balanced(dev, bits, k, n, m, monkeypatch):
     _gemm_check(dev, _case(k, n, bits, seed=500 + bits + m), m, "fp16", bias=(m != 1))
 
 
+def test_config1_merged_gate_up_m1_to_m4(dev):
+    """Config 1's merged gate|up layer (4096 -> 28672, 3-bit) at its real shape: k_gemv_stream at
+    M = 1, 2 and the balanced kernel at M = 3, 4, all against one oracle dequantization."""
+    gu = synth.layer_calls(1)[2][0]
+    cd = gu.to(dev)
+    prep = ops.gptq_prepare(cd.qweight, cd.qzeros, cd.scales, None, gu.bits, gu.group_size)
+    w = _oracle_w(gu, "fp16")
+    for m in (1, 2, 3, 4):
+        x = synth.activations(m, gu.in_features, torch.float16, seed=600 + m)
+        y = ops.gptq_gemm(x.to(dev), prep)
+        ref = og.linear_ref(_np(x), w, "fp16", None)
+        r = _rel(_np(y.float()), ref)
+        assert r <= 1e-2, f"M={m}: max rel err {r:.3e}"
+
+
 # K = 8192 at M = 4: x and its k-block sums take 70 KB of LDS (86 KB with the balanced kernel's
 # partial sums), above the 64 KB of earlier CDNA parts.
 @pytest.mark.parametrize("bal", ["0", "1"])
