@@ -53,6 +53,16 @@ enum {
 int oc_abi_version(void);
 const char* oc_last_error(void);
 
+/* Plan pinning for tests and tuning (no counterpart in the reference).  Every launch plan
+ * (kernel family, waves, tile height, K split) is a fixed function of the shape and the device;
+ * oc_set_plan_override pins one knob by its OC_* name (OC_ERR_INVALID for an unknown name) until
+ * oc_clear_plan_overrides.  Not for concurrent use with launches.  Workspace sizes may change
+ * with an override: oc_plan_generation() changes on every set/clear so callers that cache
+ * workspace sizes know to recompute them.  Host only. */
+int oc_set_plan_override(const char* name, int value);
+void oc_clear_plan_overrides(void);
+int oc_plan_generation(void);
+
 /* ---------------------------------------------------------------- GPTQ parity tools -------- */
 
 /* codes[N, K] = unpacked qweight (int32 in [0, 2^b-1]).
@@ -98,6 +108,13 @@ int oc_gptq_prepare(const int32_t* qweight, const int32_t* qzeros, const uint16_
 
 /* Workspace bytes oc_gptq_gemm needs for this call (host only). */
 size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int group_size, int has_perm);
+
+/* Text description of the launches oc_gptq_gemm makes for this call (kernel names and plan
+ * parameters, e.g. "k_gemm mt=4 cs=4 tiles=1024 split_tiles=64 S=4 kper=10 + k_gemm_fixup"),
+ * written to buf (len bytes, host memory).  Host only; for tests and reports (no counterpart in
+ * the reference). */
+int oc_gptq_describe_plan(int M, int K, int N, int bits, int group_size, int has_perm, char* buf,
+                          int len);
 
 /* y[M, N] = x[M, K] @ dequant(W)^T (+ bias), fp32 accumulation, y in act_dtype.
  * x row stride is K.  perm: int32 [K] from oc_gptq_prepare or NULL.  bias: [N] act_dtype or NULL.

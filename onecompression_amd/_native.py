@@ -24,6 +24,9 @@ c_size_t_p = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES = {
     "oc_abi_version": (c_int, []),
     "oc_last_error": (c_char_p, []),
+    "oc_set_plan_override": (c_int, [c_char_p, c_int]),
+    "oc_clear_plan_overrides": (None, []),
+    "oc_plan_generation": (c_int, []),
     "oc_gptq_unpack_codes": (c_int, [P, c_int, c_int, c_int, P, P]),
     "oc_gptq_unpack_zeros": (c_int, [P, c_int, c_int, c_int, c_int, P, P]),
     "oc_gptq_dequant": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P, P]),
@@ -31,6 +34,7 @@ SIGNATURES = {
     "oc_gptq_prepare": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P, P, P,
                                 c_int_p, P]),
     "oc_gptq_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "oc_gptq_describe_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_char_p, c_int]),
     "oc_gptq_gemm": (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P, P,
                              c_size_t, P]),
     "oc_gptq_grouped_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
@@ -98,6 +102,27 @@ def call(name: str, *args) -> int:
     if rc != 0:
         raise OCError(rc, name, lib.oc_last_error().decode(errors="replace"))
     return rc
+
+
+def set_plan_override(name: str, value: int) -> None:
+    """Pin one launch-plan knob (an ``OC_*`` name) until :func:`clear_plan_overrides` (tests)."""
+    call("oc_set_plan_override", name.encode(), int(value))
+
+
+def clear_plan_overrides() -> None:
+    load().oc_clear_plan_overrides()
+
+
+def plan_generation() -> int:
+    """Changes whenever an override is set or cleared (workspace sizes may change with it)."""
+    return load().oc_plan_generation()
+
+
+def describe_gptq_plan(m: int, k: int, n: int, bits: int, group_size: int, has_perm: bool = False) -> str:
+    """The launches oc_gptq_gemm makes for this call, as text (host only)."""
+    buf = ctypes.create_string_buffer(256)
+    call("oc_gptq_describe_plan", m, k, n, bits, group_size, int(has_perm), buf, 256)
+    return buf.value.decode()
 
 
 def last_error() -> str:

@@ -281,10 +281,6 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
   }
 }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
 
 constexpr size_t kSignLds = 64 * 1024;
 
@@ -292,7 +288,7 @@ constexpr size_t kSignLds = 64 * 1024;
 // (the rank-side stage has few row tiles), no more than the units allow, and
 // an LDS x slot per wave.
 int sign_waves(int RT, int NU, int M, int UK) {
-  const int e = env_int("OC_SIGN_W", 0);
+  const int e = oc::knob("OC_SIGN_W", 0);
   int w = (e == 4 || e == 8 || e == 16) ? e : (RT >= 768 ? 4 : (RT >= 384 ? 8 : 16));
   while (w > 4 && w > NU) w /= 2;
   const size_t slot = (size_t)M * (UK * 128 + 8) * 2;
@@ -376,7 +372,7 @@ namespace {
 // Several terms: one launch per term, every tile written as an fp32 partial
 // (post-scaled) into its slot, then one fixup sums the slots and adds bias.
 // ---------------------------------------------------------------------------
-int sign_gemm_min_m() { return env_int("OC_SIGN_GEMM_MIN_M", kSignGemvMaxM + 1); }
+int sign_gemm_min_m() { return oc::knob("OC_SIGN_GEMM_MIN_M", kSignGemvMaxM + 1); }
 
 int round8(int v) { return (v + 7) / 8 * 8; }
 
@@ -410,10 +406,10 @@ struct SignGemmPlan {
 SignGemmPlan plan_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R) {
   SignGemmPlan p;
   const SignLayout L = make_sign_layout(R, terms[0].Kd);
-  const int e = env_int("OC_GEMM_MT", 0);
+  const int e = oc::knob("OC_GEMM_MT", 0);
   p.mt = (e == 1 || e == 2 || e == 4) ? e : oc_gemm::gemm_tile_height(M, L.RT * 16);
   // several terms are summed through partial slots: no K split inside a term
-  p.gp = oc_gemm::plan_gemm(M, L.RT * 16, L.K_pad, n_terms > 1 ? 1 : env_int("OC_GEMM_SPLIT", 0), p.mt);
+  p.gp = oc_gemm::plan_gemm(M, L.RT * 16, L.K_pad, n_terms > 1 ? 1 : oc::knob("OC_GEMM_SPLIT", 0), p.mt);
   size_t off = 0;
   for (int i = 0; i < n_terms; ++i) {
     p.xs_off[i] = off;

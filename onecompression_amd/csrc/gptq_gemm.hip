@@ -16,6 +16,7 @@
 // ~50 us per call.)
 //
 // Large M: k_gemm below (x tiles staged in LDS, weights dequantised in registers).
+#include <stdio.h>
 #include <stdlib.h>
 
 #include "gemm_core.h"
@@ -1234,19 +1235,15 @@ struct SkinnyPlan {
   int nt, mb, S, ups, ngroups;
 };
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
 
 SkinnyPlan plan_skinny(const oc::Layout& L, int M) {
   SkinnyPlan p;
   p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  p.nt = env_int("OC_SKINNY_NT", L.NT >= 512 ? 4 : 2);
+  p.nt = oc::knob("OC_SKINNY_NT", L.NT >= 512 ? 4 : 2);
   if (p.nt != 2 && p.nt != 4) p.nt = 2;
   p.ngroups = (L.NT + p.nt - 1) / p.nt;
   // enough workgroups to cover 256 CUs about twice, but at least one unit per wave
-  int S = env_int("OC_SKINNY_S", 0);
+  int S = oc::knob("OC_SKINNY_S", 0);
   if (S <= 0) {
     S = 1;
     while (p.ngroups * S < 512 && L.NU / (S * 2) >= 4) S *= 2;
@@ -1306,14 +1303,14 @@ GemvPlan plan_gemv(const oc::Layout& L, int M, int gs) {
   p.xch = xc <= 1 ? 1 : (xc <= 4 ? 4 : (xc <= 8 ? 8 : 16));
   // Two n-tiles per workgroup when there are enough column groups left to
   // fill the GPU: fewer, longer waves (measured better on 3-bit gate/up).
-  const int nt_env = env_int("OC_GEMV_NT", 0);
+  const int nt_env = oc::knob("OC_GEMV_NT", 0);
   p.nt = (p.xch == 1 && (nt_env == 2 || (nt_env == 0 && (L.NT + 1) / 2 >= 384))) ? 2 : 1;
   p.ngroups = (L.NT + p.nt - 1) / p.nt;
   // One workgroup streams the whole K of its columns; few column groups get
   // more waves per workgroup.  Each wave owns an x slot of M x (128U + 8) halfs.
   // A CU holds one 16-wave workgroup of this kernel (its registers), so more
   // column groups than CUs take 8 waves: one round of workgroups, not two.
-  int w = env_int("OC_GEMV_W", 0);
+  int w = oc::knob("OC_GEMV_W", 0);
   if (w != 4 && w != 8 && w != 16) w = (p.ngroups > oc_device_cus() || p.nt == 2) ? 8 : 16;
   if (p.cs == 1 && w == 16) w = 8;
   if (p.xch > 1 && w == 16) w = 8;
@@ -1321,8 +1318,8 @@ GemvPlan plan_gemv(const oc::Layout& L, int M, int gs) {
   const size_t slot = (size_t)M * (L.U * 128 + 8) * 2;
   while (w > 4 && slot * w > kGemvLds) w /= 2;
   p.w = w;
-  p.deep = env_int("OC_GEMV_DEEP", 0);
-  int S = env_int("OC_GEMV_S", 1);
+  p.deep = oc::knob("OC_GEMV_DEEP", 0);
+  int S = oc::knob("OC_GEMV_S", 1);
   S = S < 1 ? 1 : (S > L.NU ? L.NU : S);
   p.ups = (L.NU + S - 1) / S;
   p.S = (L.NU + p.ups - 1) / p.ups;
@@ -1394,7 +1391,7 @@ constexpr size_t kStreamLds = 80 * 1024;  // two workgroups per CU (160 KB of LD
 // Waves per n-tile of k_gemv_stream (OC_GEMV_STREAM_KS = 1 or 2; default 1,
 // measured faster than two half-K waves on the configs' wide layers).
 int stream_ksplit(const oc::Layout& L) {
-  const int e = env_int("OC_GEMV_STREAM_KS", 0);
+  const int e = oc::knob("OC_GEMV_STREAM_KS", 0);
   const int ks = (e == 1 || e == 2) ? e : 1;
   return (L.NU % ks) == 0 ? ks : 1;
 }
@@ -1408,7 +1405,7 @@ size_t stream_lds(const oc::Layout& L, int M) {
 // powers of two >= 128 and an even number of units.  OC_GEMM_STREAM=0 turns
 // it off, =1 forces it where it applies.
 bool use_gemm_stream(const oc::Layout& L, int M, int gs) {
-  const int e = env_int("OC_GEMM_STREAM", -1);
+  const int e = oc::knob("OC_GEMM_STREAM", -1);
   if (e == 0 || M > 32 || gs < 128 || log2_exact(gs) < 0 || (L.NU % 2) != 0) return false;
   if (e == 1) return true;
   // measured: k_gemv is faster for 4 < M <= 12, the streaming GEMM from 13 rows
@@ -1438,11 +1435,11 @@ int dispatch_gemm_stream(int bits, int M, const oc::Layout& L, const StreamArgs&
 // >= 128.  OC_GEMV_STREAM=0 turns it off, =1 forces it (up to M = 8) where it
 // applies; OC_GEMV_STREAM_D picks the depth (2 or 4).
 int stream_depth(const oc::Layout& L, int M, int gs) {
-  const int e = env_int("OC_GEMV_STREAM", -1);
+  const int e = oc::knob("OC_GEMV_STREAM", -1);
   if (e == 0 || M > (e == 1 ? 8 : 4) || gs < 128 || log2_exact(gs) < 0) return 0;
   if (stream_lds(L, M) > kStreamLds) return 0;
   if (e != 1 && L.NT < 1024) return 0;
-  const int de = env_int("OC_GEMV_STREAM_D", 0);
+  const int de = oc::knob("OC_GEMV_STREAM_D", 0);
   const int ks = stream_ksplit(L);
   const int nu = L.NU / ks;
   int d = (de == 2 || de == 4) ? de : ((nu % 4) == 0 ? 4 : 2);
@@ -1458,7 +1455,7 @@ int stream_depth(const oc::Layout& L, int M, int gs) {
 // configs' wide layers even where its CUs are unevenly loaded).
 // OC_GEMV_STREAM_BAL=0 turns it off, =1 forces it where T <= 8.
 int stream_bal_tiles(const oc::Layout& L, int bits, int M, int ks) {
-  const int e = env_int("OC_GEMV_STREAM_BAL", -1);
+  const int e = oc::knob("OC_GEMV_STREAM_BAL", -1);
   if (e == 0 || ks != 1 || (e != 1 && M < 3)) return 0;
   const int cus = oc_device_cus();
   const int t = (L.NT + cus - 1) / cus;
@@ -1513,7 +1510,7 @@ int dispatch_stream(int bits, int d, int M, const oc::Layout& L, StreamArgs a, h
 // Tile height of the GEMM for M rows (64 MT rows, 256 columns): see
 // gemm_tile_height; only 256-row tiles for groups that are not multiples of 128.
 int gemm_mt(int M, int N_pad, int gs) {
-  const int e = env_int("OC_GEMM_MT", 0);
+  const int e = oc::knob("OC_GEMM_MT", 0);
   if ((gs % 128) != 0) return 4;
   if (e == 1 || e == 2 || e == 4) return e;
   return gemm_tile_height(M, N_pad);
@@ -1523,7 +1520,7 @@ int gemm_mt(int M, int N_pad, int gs) {
 // for groups that are not multiples of 128, which only have 256-row tiles);
 // the skinny kernel below that.  OC_GEMM_MIN_M overrides the threshold.
 bool use_gemm(int M, int N_pad, int gs) {
-  const int e = env_int("OC_GEMM_MIN_M", 0);
+  const int e = oc::knob("OC_GEMM_MIN_M", 0);
   if (e > 0) return M >= e;
   if ((gs % 128) != 0) return M >= 128;
   return M > 32 || (M > kGemvMaxM && (N_pad + 255) / 256 >= 64);
@@ -1548,12 +1545,43 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
   }
   if (use_gemm(M, L.N_pad, oc::eff_group(group_size, K))) {
     const int mt = gemm_mt(M, L.N_pad, oc::eff_group(group_size, K));
-    return ws + align256(plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0), mt).part_bytes);
+    return ws + align256(plan_gemm(M, L.N_pad, L.K_pad, oc::knob("OC_GEMM_SPLIT", 0), mt).part_bytes);
   }
   const int Mc = M < kSkinnyMaxM ? M : kSkinnyMaxM;
   const SkinnyPlan p = plan_skinny(L, Mc);
   if (p.S > 1) ws += align256((size_t)p.S * Mc * L.N_pad * 4);
   return ws;
+}
+
+extern "C" int oc_gptq_describe_plan(int M, int K, int N, int bits, int group_size, int has_perm, char* buf,
+                                     int len) {
+  OC_REQUIRE(buf && len > 0, OC_ERR_INVALID, "null buffer");
+  OC_REQUIRE(bits == 2 || bits == 3 || bits == 4 || bits == 8, OC_ERR_UNSUPPORTED, "unsupported bits=%d", bits);
+  OC_REQUIRE(M > 0 && K > 0 && N > 0 && K % 32 == 0, OC_ERR_INVALID, "bad shape M=%d K=%d N=%d", M, K, N);
+  const oc::Layout L = oc::make_layout(bits, K, N);
+  const int gs = oc::eff_group(group_size, K);
+  const char* g = has_perm ? "k_gather + " : "";
+  const int sd = M <= kGemvMaxM ? stream_depth(L, M, gs) : 0;
+  if (sd == 0 && use_gemm_stream(L, M, gs)) {
+    snprintf(buf, len, "%sk_gemm_stream mb=%d", g, M <= 16 ? 1 : 2);
+  } else if (M <= kGemvMaxM && sd > 0) {
+    const int t = stream_bal_tiles(L, bits, M, stream_ksplit(L));
+    if (t > 0) snprintf(buf, len, "%sk_gemv_stream_bal d=%d tiles_per_wg=%d", g, sd, t);
+    else snprintf(buf, len, "%sk_gemv_stream d=%d ks=%d", g, sd, stream_ksplit(L));
+  } else if (M <= kGemvMaxM) {
+    const GemvPlan p = plan_gemv(L, M, gs);
+    snprintf(buf, len, "%sk_gemv nt=%d w=%d S=%d%s", g, p.nt, p.w, p.S, p.S > 1 ? " + k_splitk_reduce" : "");
+  } else if (use_gemm(M, L.N_pad, gs)) {
+    const int mt = gemm_mt(M, L.N_pad, gs);
+    const GemmPlan gp = plan_gemm(M, L.N_pad, L.K_pad, oc::knob("OC_GEMM_SPLIT", 0), mt);
+    snprintf(buf, len, "%sk_gemm mt=%d cs=%d tiles=%d split_tiles=%d S=%d kper=%d%s", g, mt, (gs % 128) ? 1 : 4,
+             gp.tiles_main, gp.split_tiles, gp.S, gp.kper, gp.split_tiles ? " + k_gemm_fixup" : "");
+  } else {
+    const SkinnyPlan p = plan_skinny(L, M < kSkinnyMaxM ? M : kSkinnyMaxM);
+    snprintf(buf, len, "%sk_skinny chunks=%d S=%d%s", g, (M + kSkinnyMaxM - 1) / kSkinnyMaxM, p.S,
+             p.S > 1 ? " + k_splitk_reduce" : "");
+  }
+  return 0;
 }
 
 namespace {
@@ -1672,7 +1700,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     g.NKB = L.K_pad / 128;
     const bool cs4 = (gs % 128) == 0;
     const int mt = gemm_mt(M, L.N_pad, gs);
-    const GemmPlan gp = plan_gemm(M, L.N_pad, L.K_pad, env_int("OC_GEMM_SPLIT", 0), mt);
+    const GemmPlan gp = plan_gemm(M, L.N_pad, L.K_pad, oc::knob("OC_GEMM_SPLIT", 0), mt);
     g.post = nullptr;
     g.ldx = K;
     g.ldy = ldy;
@@ -1811,12 +1839,12 @@ GroupPlan plan_group(const oc_gptq_part* parts, int n_parts, int M, int K) {
     int blocks = 0;
     for (int i = 0; i < n_parts; ++i) {
       const int NT = oc::make_layout(parts[i].bits, K, parts[i].N).NT;
-      const int nt = (g.xch == 1 && 2 * parts[i].bits <= bmax && NT >= 2 && env_int("OC_GROUP_NT", 2) == 2) ? 2 : 1;
+      const int nt = (g.xch == 1 && 2 * parts[i].bits <= bmax && NT >= 2 && oc::knob("OC_GROUP_NT", 2) == 2) ? 2 : 1;
       g.nt[i] = nt;
       g.ntmax = nt > g.ntmax ? nt : g.ntmax;
       blocks += (NT + nt - 1) / nt;
     }
-    if ((blocks > oc_device_cus() || g.ntmax == 2) && g.w > 8 && env_int("OC_GEMV_W", 0) == 0) g.w = 8;
+    if ((blocks > oc_device_cus() || g.ntmax == 2) && g.w > 8 && oc::knob("OC_GEMV_W", 0) == 0) g.w = 8;
     if (g.xch > 1 && g.w > 8) g.w = 8;
     while (g.w > 4 && slot * g.w > kGemvLds) g.w /= 2;
     const size_t xb = slot * g.w, rb = (size_t)g.w * g.ntmax * 4 * 64 * 4;
@@ -2000,7 +2028,7 @@ MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
   // rows per run: one for a single token (its slots name distinct experts); else 4, or 16
   // when the pairs spread over the experts give more than 4 per expert on average; beyond
   // 64 pairs, sorted runs of up to 16 (OC_MOE_RM=1: one row per pair)
-  const int rm_env = env_int("OC_MOE_RM", 0);
+  const int rm_env = oc::knob("OC_MOE_RM", 0);
   int rm = rm_env;
   if (rm != 1 && rm != 4 && rm != 16) {
     const size_t busy = pairs < (size_t)E ? pairs : (size_t)E;
@@ -2013,7 +2041,7 @@ MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
   p.w1 = 4;  // gate|up
   const int nu2 = (I + 128 * U - 1) / (128 * U);
   // down: 8 waves for long k-ranges (runs of 1 or 4 rows, groups of 128 or more)
-  int w2 = env_int("OC_MOE_W2", 0);
+  int w2 = oc::knob("OC_MOE_W2", 0);
   if (w2 != 4 && w2 != 8) w2 = nu2 >= 24 ? 8 : 4;
   if (rm == 16 || rm == kMoeSorted || gs2 % 128 != 0) w2 = 4;
   p.w2 = w2;
@@ -2086,7 +2114,7 @@ int moe_prefill(const void* x, int M, int H, int I, int E, int topk, const int32
   const int avg = pairs / busy;
   const bool cs4a = gs13 % 128 == 0, cs4b = gs2 % 128 == 0;
   int mt = avg >= 256 ? 4 : (avg >= 128 ? 2 : 1);
-  const int mt_env = env_int("OC_MOE_GEMM_MT", 0);
+  const int mt_env = oc::knob("OC_MOE_GEMM_MT", 0);
   if (mt_env == 1 || mt_env == 2 || mt_env == 4) mt = mt_env;
   if (!cs4a || !cs4b) mt = 4;  // the GEMM for groups below 128 is built for 256-row tiles
   const int BM = 64 * mt;
@@ -2220,11 +2248,12 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
     a.ups = L.NU;
     a.bits = bits;
   };
-  // prefill sizes (at least 32 rows per expert on average): the large-M GEMM per run of rows
+  // The grouped large-M GEMM per run of rows (prefill sizes) is opt-in (knob OC_MOE_GEMM = 1):
+  // one test run of it once reported a wrong result whose cause has not been shown, so the
+  // default serves every size on the sorted-run GEMV path.
   {
-    const int busy = E < pairs ? E : pairs;
-    const int gm = env_int("OC_MOE_GEMM", -1);
-    if (E <= kMoeMaxE && pairs >= 32 && (gm == 1 || (gm != 0 && pairs / busy >= 32)))
+    const int gm = oc::knob("OC_MOE_GEMM", 0);
+    if (E <= kMoeMaxE && pairs >= 32 && gm == 1)
       return moe_prefill(x, M, H, I, E, topk, ids, weights, w13, w13_stride, meta13, meta13_stride, b13, w2,
                          w2_stride, meta2, meta2_stride, b2, bits, gs13, gs2, act, alpha, limit, bf16, y, ws, mp, st);
   }

@@ -550,10 +550,6 @@ int had_chunk_log2(int n, int K) {
 
 }  // namespace
 
-static int env_int_had(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
 
 extern "C" int oc_hadamard_order(int n) { return n > 0 ? pick_order(n) : 0; }
 
@@ -594,7 +590,7 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
   const int Lh = n / K;
   const char *xb = (const char*)x, *yb = (const char*)y;
   const bool overlap = xb < yb + (size_t)M * ld_y * 2 && yb < xb + (size_t)M * ld_x * 2;
-  const int mm_max = env_int_had("OC_HAD_MM_M", 16);
+  const int mm_max = oc::knob("OC_HAD_MM_M", 16);
   if (M <= mm_max && Lh >= 16 && K <= 16 * kHadMmMaxKT && n <= kHadMmMaxN && !overlap && vx &&
       ((uintptr_t)y & 1) == 0) {
     hipStream_t st = (hipStream_t)stream;

@@ -14,6 +14,8 @@ namespace oc {
 
 int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);
+// Plan knob `name` (an OC_* name) if a test pinned it with oc_set_plan_override, else dflt.
+int knob(const char* name, int dflt);
 
 #define OC_REQUIRE(cond, code, ...)                 \
   do {                                              \

@@ -98,7 +98,7 @@ class PreparedGPTQ:
     bits: int
     group_size: int
     num_groups: int
-    _ws: dict = field(default_factory=dict, repr=False)  # workspace bytes per M
+    _ws: dict = field(default_factory=dict, repr=False)  # workspace bytes per (M, plan generation)
 
 
 def gptq_layout(k: int, n: int, bits: int):
@@ -152,11 +152,12 @@ def gptq_gemm(x: torch.Tensor, prep: PreparedGPTQ, bias: Optional[torch.Tensor] 
         out = torch.empty((m, n), dtype=x.dtype, device=dev)
     else:
         _need(out, "out", x.dtype, (m, n), dev)
-    ws_bytes = prep._ws.get(m)
+    key = (m, N.plan_generation())
+    ws_bytes = prep._ws.get(key)
     if ws_bytes is None:
         ws_bytes = N.load().oc_gptq_workspace_bytes(m, k, n, prep.bits, prep.group_size,
                                                     int(prep.perm is not None))
-        prep._ws[m] = ws_bytes
+        prep._ws[key] = ws_bytes
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     N.call("oc_gptq_gemm", _ptr(x2), m, k, n, _ptr(prep.packed), _ptr(prep.meta), _ptr(prep.perm),
            prep.bits, prep.group_size, _DT[x.dtype], _ptr(bias), _ptr(out), _ptr(ws), ws_bytes,

@@ -29,3 +29,12 @@ def dev():
     if not torch.cuda.is_available():
         pytest.fail("GPU test collected on a host without a GPU; run with -m 'not gpu'")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def plan():
+    """Pin launch-plan knobs for one test: plan("OC_GEMM_MT", 2).  Cleared afterwards."""
+    from onecompression_amd import _native as N
+
+    yield N.set_plan_override
+    N.clear_plan_overrides()

@@ -136,30 +136,28 @@ def test_gemm_config2_act_order_m16(dev):
     _gemm_check(dev, c, 16, "fp16")
 
 
-def test_gemm_repeatable_split_k(dev, monkeypatch):
+def test_gemm_repeatable_split_k(dev, plan):
     """The split-K path (forced) is deterministic and matches the unsplit one."""
     c = synth.config_cases(1)[1].to(dev)  # k_proj 4096 -> 1024
     prep = ops.gptq_prepare(c.qweight, c.qzeros, c.scales, None, c.bits, 128)
     x = synth.activations(3, 4096).to(dev)
     y1 = ops.gptq_gemm(x, prep).clone()
-    monkeypatch.setenv("OC_GEMV_S", "4")
-    prep._ws.clear()
+    plan("OC_GEMV_S", "4")
     y4 = ops.gptq_gemm(x, prep)
     for _ in range(3):
         assert torch.equal(ops.gptq_gemm(x, prep), y4)
     torch.cuda.synchronize()
     assert float((y4.float() - y1.float()).abs().max()) <= 1e-2 * float(y1.float().abs().max())
-    prep._ws.clear()
 
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("w,nt", [(4, 1), (8, 1), (16, 1), (4, 2), (8, 2), (16, 2)])
-def test_gemv_plan_variants(dev, monkeypatch, bits, w, nt):
+def test_gemv_plan_variants(dev, plan, bits, w, nt):
     """Every GEMV launch shape (waves per workgroup x n-tiles per wave), with
     several k-units per wave, M = 1 and M = 7 (x rows bounced through LDS by a
     subset of lanes)."""
-    monkeypatch.setenv("OC_GEMV_W", str(w))
-    monkeypatch.setenv("OC_GEMV_NT", str(nt))
+    plan("OC_GEMV_W", str(w))
+    plan("OC_GEMV_NT", str(nt))
     c = _case(4096, 256 if bits != 3 else 320, bits, seed=60 + bits)
     for m in (1, 7):
         _gemm_check(dev, c, m, "fp16", bias=m == 7)
@@ -167,19 +165,19 @@ def test_gemv_plan_variants(dev, monkeypatch, bits, w, nt):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("m", [17, 32, 48, 64, 65, 100, 128, 130, 200])
-def test_gemm_mid_m(dev, bits, m, monkeypatch):
+def test_gemm_mid_m(dev, bits, m, plan):
     """16 < M < 256 on the tiled GEMM (tile height 64, 128 or 256 by M), with bias on even M."""
-    monkeypatch.setenv("OC_GEMM_MIN_M", "17")
+    plan("OC_GEMM_MIN_M", "17")
     _gemm_check(dev, _case(2048, 320 if bits == 3 else 256, bits, seed=70 + bits + m), m, "fp16", bias=m % 2 == 0)
 
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("mt", ["1", "2", "4"])
-def test_gemm_tile_heights(dev, monkeypatch, bits, mt):
+def test_gemm_tile_heights(dev, plan, bits, mt):
     """Every tile height at M below, at and above it; K = 4096 on 256 columns splits the few
     tiles along K (fp32 partials, fixup kernel)."""
-    monkeypatch.setenv("OC_GEMM_MIN_M", "17")
-    monkeypatch.setenv("OC_GEMM_MT", mt)
+    plan("OC_GEMM_MIN_M", "17")
+    plan("OC_GEMM_MT", mt)
     c = _case(4096, 320 if bits == 3 else 256, bits, seed=80 + bits)
     for m in (24, 96, 160):
         _gemm_check(dev, c, m, "fp16" if m != 96 else "bf16", bias=m == 96)
@@ -188,10 +186,10 @@ def test_gemm_tile_heights(dev, monkeypatch, bits, mt):
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("gs,act,dtype,k", [(64, False, "fp16", 1024), (32, False, "bf16", 1056),
                                             (128, True, "bf16", 2048), (-1, False, "fp16", 1056)])
-def test_gemm_mid_groups(dev, monkeypatch, bits, gs, act, dtype, k):
+def test_gemm_mid_groups(dev, plan, bits, gs, act, dtype, k):
     """Tiled GEMM at mid M with groups of 32/64 (256-row tiles), act-order, one group and K not
     a multiple of the k-unit."""
-    monkeypatch.setenv("OC_GEMM_MIN_M", "17")
+    plan("OC_GEMM_MIN_M", "17")
     c = _case(k, 320 if bits == 3 else 272, bits, gs, act, seed=90 + bits)
     for m in (40, 128):
         _gemm_check(dev, c, m, dtype, bias=m == 40)
@@ -217,7 +215,7 @@ def test_gemm_large_m_config4_shape(dev):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-def test_gemm_split_tail(dev, monkeypatch, dtype):
+def test_gemm_split_tail(dev, plan, dtype):
     """260 tiles of 256 x 256 on a 256-CU part: 256 whole tiles plus 4 tiles cut
     along K whose fp32 partials k_gemm_fixup sums (with bias).  The split result
     matches the unsplit launch and, on the tail tiles' columns, the oracle."""
@@ -230,11 +228,9 @@ def test_gemm_split_tail(dev, monkeypatch, dtype):
     b = (torch.randn(n) * 0.1).to(td).to(dev)
     y = ops.gptq_gemm(x, prep, b)
     assert torch.equal(ops.gptq_gemm(x, prep, b), y)  # deterministic split order
-    monkeypatch.setenv("OC_GEMM_SPLIT", "1")
-    prep._ws.clear()
+    plan("OC_GEMM_SPLIT", "1")
     y1 = ops.gptq_gemm(x, prep, b)
     torch.cuda.synchronize()
-    prep._ws.clear()
     ref_scale = float(y1.float().abs().max())
     assert float((y.float() - y1.float()).abs().max()) <= 1e-2 * ref_scale
     n0, n1 = 65536 - 256, n  # last whole tile and the 4 split tiles
@@ -260,7 +256,7 @@ def test_gemm_streaming_wide(dev, bits, m):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("case", ["act", "bf16", "g256", "narrow_forced"])
-def test_gemm_streaming_variants(dev, bits, case, monkeypatch):
+def test_gemm_streaming_variants(dev, bits, case, plan):
     if case == "act":
         _gemm_check(dev, _case(1024, 16384, bits, 128, True, seed=70 + bits), 2, "fp16", bias=True)
     elif case == "bf16":
@@ -268,7 +264,7 @@ def test_gemm_streaming_variants(dev, bits, case, monkeypatch):
     elif case == "g256":
         _gemm_check(dev, _case(1024, 16384, bits, 256, False, seed=90 + bits), 1, "fp16")
     else:  # forced on a narrow layer: fewer n-tiles than one workgroup's 4 waves in the last group
-        monkeypatch.setenv("OC_GEMV_STREAM", "1")
+        plan("OC_GEMV_STREAM", "1")
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=95 + bits), 5, "fp16", bias=True)
 
 
@@ -284,9 +280,9 @@ BAL_SHAPES = [(4096, 28672, 1), (512, 16384 + 32, 3), (1024, 2048 + 32, 4), (512
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("k,n,m", BAL_SHAPES)
-def test_gemm_streaming_balanced(dev, bits, k, n, m, monkeypatch):
-    monkeypatch.setenv("OC_GEMV_STREAM", "1")
-    monkeypatch.setenv("OC_GEMV_STREAM_BAL", "1")
+def test_gemm_streaming_balanced(dev, bits, k, n, m, plan):
+    plan("OC_GEMV_STREAM", "1")
+    plan("OC_GEMV_STREAM_BAL", "1")
     _gemm_check(dev, _case(k, n, bits, seed=500 + bits + m), m, "fp16", bias=(m != 1))
 
 
@@ -308,15 +304,15 @@ def test_config1_merged_gate_up_m1_to_m4(dev):
 # K = 8192 at M = 4: x and its k-block sums take 70 KB of LDS (86 KB with the balanced kernel's
 # partial sums), above the 64 KB of earlier CDNA parts.
 @pytest.mark.parametrize("bal", ["0", "1"])
-def test_gemm_streaming_large_lds(dev, bal, monkeypatch):
-    monkeypatch.setenv("OC_GEMV_STREAM_BAL", bal)
+def test_gemm_streaming_large_lds(dev, bal, plan):
+    plan("OC_GEMV_STREAM_BAL", bal)
     _gemm_check(dev, _case(8192, 16384 + 32, 4, seed=540), 4, "fp16", bias=True)
 
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("case", ["act", "bf16", "g256"])
-def test_gemm_streaming_balanced_variants(dev, bits, case, monkeypatch):
-    monkeypatch.setenv("OC_GEMV_STREAM_BAL", "1")
+def test_gemm_streaming_balanced_variants(dev, bits, case, plan):
+    plan("OC_GEMV_STREAM_BAL", "1")
     if case == "act":
         _gemm_check(dev, _case(1024, 17408, bits, 128, True, seed=510 + bits), 2, "fp16", bias=True)
     elif case == "bf16":
@@ -354,7 +350,7 @@ def test_gemm_streaming_mid_m(dev, bits, m):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("case", ["act", "bf16", "g256", "long_k_m4", "narrow_forced"])
-def test_gemm_streaming_mid_m_variants(dev, bits, case, monkeypatch):
+def test_gemm_streaming_mid_m_variants(dev, bits, case, plan):
     if case == "act":
         _gemm_check(dev, _case(1024, 16384, bits, 128, True, seed=130 + bits), 20, "fp16", bias=True)
     elif case == "bf16":
@@ -364,7 +360,7 @@ def test_gemm_streaming_mid_m_variants(dev, bits, case, monkeypatch):
     elif case == "long_k_m4":
         _gemm_check(dev, _case(14336, 16384, bits, seed=155 + bits), 4, "fp16")
     else:
-        monkeypatch.setenv("OC_GEMM_STREAM", "1")
+        plan("OC_GEMM_STREAM", "1")
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=160 + bits), 30, "fp16", bias=True)
 
 

@@ -162,9 +162,9 @@ def test_moe_long_down(dev, bits, inter, m):
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
 @pytest.mark.parametrize("rows", [4, 16])
-def test_moe_runs_of_rows(dev, monkeypatch, bits, rows):
+def test_moe_runs_of_rows(dev, plan, bits, rows):
     """Runs of up to 4 or 16 pairs on one expert (OC_MOE_RM forces the run length)."""
-    monkeypatch.setenv("OC_MOE_RM", str(rows))
+    plan("OC_MOE_RM", str(rows))
     E, H, I, k, gs, m = 3, 256, 128, 2, 128, 20
     cases, ref = _build(E, H, I, bits, gs, True, "fp16", seed=70 + bits)
     ex = _prepare(cases, bits, gs, dev)
@@ -215,11 +215,11 @@ def test_vllm_fused_moe_layer(dev, act, bits):
 
 
 @pytest.mark.parametrize("bits,act", [(4, "silu"), (3, "gpt_oss"), (2, "silu"), (8, "gelu_pytorch_tanh")])
-def test_moe_sorted_runs_many_tokens(dev, monkeypatch, bits, act):
+def test_moe_sorted_runs_many_tokens(dev, plan, bits, act):
     """Beyond 64 pairs the pairs are sorted by expert on the device and served 16 rows per weight
     read (OC_MOE_GEMM=0 keeps this call off the prefill GEMM path): same output bits as one row
     per pair (OC_MOE_RM=1), and the oracle's values."""
-    monkeypatch.setenv("OC_MOE_GEMM", "0")
+    plan("OC_MOE_GEMM", "0")
     E, H, I, k, gs, m = 8, 256, 128, 4, 128, 300
     bias = act == "gpt_oss"
     cases, ref = _build(E, H, I, bits, gs, bias, "fp16", seed=110 + bits)
@@ -230,7 +230,7 @@ def test_moe_sorted_runs_many_tokens(dev, monkeypatch, bits, act):
     idx[7, :] = E  # a token with no valid slot
     xd, idd, wd = x.to(dev), idx.to(dev), w.to(dev)
     y = moe.moe_forward(xd, idd, wd, ex, act)
-    monkeypatch.setenv("OC_MOE_RM", "1")
+    plan("OC_MOE_RM", "1")
     y1 = moe.moe_forward(xd, idd, wd, ex, act)
     assert torch.equal(y, y1)
     want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref,
@@ -244,12 +244,13 @@ def test_moe_sorted_runs_many_tokens(dev, monkeypatch, bits, act):
 @pytest.mark.parametrize("bits,act,gs,dt", [(4, "silu", 128, "fp16"), (3, "gpt_oss", 128, "fp16"),
                                             (2, "gelu_pytorch_tanh", 64, "fp16"), (8, "silu", 128, "bf16")])
 @pytest.mark.parametrize("mt", [0, 1, 2])
-def test_moe_prefill_gemm(dev, monkeypatch, bits, act, gs, dt, mt):
+def test_moe_prefill_gemm(dev, plan, bits, act, gs, dt, mt):
     """Prefill sizes (>= 32 rows per expert): rows sorted by expert, the large-M GEMM per run of
     64 MT rows (MT forced for coverage), against the oracle; tokens with an invalid slot and with
     no valid slot."""
+    plan("OC_MOE_GEMM", 1)
     if mt:
-        monkeypatch.setenv("OC_MOE_GEMM_MT", str(mt))
+        plan("OC_MOE_GEMM_MT", str(mt))
     E, H, I, k, m = 4, 256, 160, 2, 130
     bias = act == "gpt_oss"
     cases, ref = _build(E, H, I, bits, gs, bias, dt, seed=130 + bits)
@@ -265,25 +266,31 @@ def test_moe_prefill_gemm(dev, monkeypatch, bits, act, gs, dt, mt):
     assert np.all(y[4] == 0.0)
     err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
     assert err <= (2e-2 if dt == "bf16" else 1e-2), err
+    # regression bound well below the bar (measured ~7e-4 fp16): a partial corruption of a few
+    # rows or k-blocks shows here even when it stays under 1e-2
+    assert err <= (8e-3 if dt == "bf16" else 2e-3), err
 
 
-def test_moe_prefill_matches_runs_path(dev, monkeypatch):
+def test_moe_prefill_matches_runs_path(dev, plan):
     """The prefill GEMM path and the 16-row run path agree within the bar on the same call."""
     E, H, I, k, m, bits = 4, 512, 256, 2, 200, 4
     cases, ref = _build(E, H, I, bits, 128, False, "fp16", seed=140)
     ex = _prepare(cases, bits, 128, dev)
     x = synth.activations(m, H, torch.float16, seed=23).to(dev)
     idx, w = _routing(m, k, E, seed=24)
+    plan("OC_MOE_GEMM", 1)
     ya = moe.moe_forward(x, idx.to(dev), w.to(dev), ex, "silu").float()
-    monkeypatch.setenv("OC_MOE_GEMM", "0")
+    plan("OC_MOE_GEMM", "0")
     yb = moe.moe_forward(x, idx.to(dev), w.to(dev), ex, "silu").float()
     assert float((ya - yb).abs().max() / yb.abs().max()) <= 1e-2
 
 
-@pytest.mark.parametrize("m", [64, 256])
-def test_moe_realistic_expert_shape(dev, m):
+@pytest.mark.parametrize("m,gemm", [(64, 0), (256, 0), (256, 1)])
+def test_moe_realistic_expert_shape(dev, plan, m, gemm):
     """Qwen3-MoE-like experts (H 2048, I 768, 16 experts, top-4, 4-bit g128): 16-row sorted runs
-    at M = 64 (16 rows per expert), the prefill GEMM at M = 256 (64 per expert)."""
+    at M = 64 (16 rows per expert) and M = 256 (64 per expert), and the opt-in prefill GEMM at
+    M = 256."""
+    plan("OC_MOE_GEMM", gemm)
     E, H, I, k, gs, bits = 16, 2048, 768, 4, 128, 4
     cases, ref = _build(E, H, I, bits, gs, False, "fp16", seed=160)
     ex = _prepare(cases, bits, gs, dev)
@@ -295,10 +302,11 @@ def test_moe_realistic_expert_shape(dev, m):
     assert err <= 1e-2, err
 
 
-@pytest.mark.parametrize("m", [3, 130])
-def test_moe_per_channel_groups(dev, m):
+@pytest.mark.parametrize("m,gemm", [(3, 0), (130, 0), (130, 1)])
+def test_moe_per_channel_groups(dev, plan, m, gemm):
     """group_size = -1 (one group over K; I = 160 is not a power of two): decode path at M = 3,
-    prefill GEMM at M = 130."""
+    sorted runs and the opt-in prefill GEMM at M = 130."""
+    plan("OC_MOE_GEMM", gemm)
     E, H, I, k, bits = 4, 256, 160, 2, 4
     cases, ref = _build(E, H, I, bits, -1, True, "fp16", seed=170)
     ex = _prepare(cases, bits, -1, dev)

@@ -100,3 +100,62 @@ def test_mdbf_l1_equals_dbf_closed_form():
     y = od.mdbf_forward(x, [path, path])
     yd = 2 * od.dbf_forward(x, s0, bp1, s2, bp3, s4, k, r, n)
     assert np.max(np.abs(y - yd)) / np.max(np.abs(yd)) < 1e-2
+
+
+def _per_scale_forward(x, path):
+    """Independent float64 evaluation of the reference's per-scale form of one MDBF path
+    (mdbf_layer.py:307-336): u = sum_k ((x * B_amp[:, k]) @ S_B^T) * Q_V[:, k], then
+    y = sum_k ((u * Q_U[:, k]) @ S_A^T) * A_amp[:, k].  No factor matrix is formed."""
+    sa = od.unpack_binary_factor(path["A_sign_packed"], path["A_shape"]).astype(np.float64)
+    sb = od.unpack_binary_factor(path["B_sign_packed"], path["B_shape"]).astype(np.float64)
+    f = lambda a: np.asarray(a, np.float64)  # noqa: E731
+    a_amp, b_amp, qu, qv = f(path["A_amp"]), f(path["B_amp"]), f(path["Q_U_amp"]), f(path["Q_V_amp"])
+    xf = f(x)
+    u = sum(((xf * b_amp[:, k]) @ sb.T) * qv[:, k] for k in range(b_amp.shape[1]))
+    return sum(((u * qu[:, k]) @ sa.T) * a_amp[:, k] for k in range(a_amp.shape[1]))
+
+
+def _mdbf_path(n, r, m, l, seed):
+    rng = np.random.default_rng(seed)
+    amp = lambda d: (np.abs(rng.normal(0, 0.3, (d, l))) + 0.05).astype(np.float32)  # noqa: E731
+    return dict(A_sign_packed=od.pack_binary(rng.choice([-1, 1], size=(n, r))), A_shape=(n, r),
+                B_sign_packed=od.pack_binary(rng.choice([-1, 1], size=(r, m))), B_shape=(r, m),
+                A_amp=amp(n), B_amp=amp(m), Q_U_amp=amp(r), Q_V_amp=amp(r))
+
+
+@pytest.mark.parametrize("l", [2, 3])
+def test_mdbf_multi_scale_matches_per_scale_form(l):
+    """The oracle's materialised-factor forward (mdbf_layer.py:278-290, :338-344) against the
+    reference's own per-scale reformulation (:307-336), evaluated independently in float64.
+    In fp32 mode (no 16-bit rounding of the amp products) the two agree to fp32 precision; in
+    fp16 mode within the per-element rounding of the factors.  Two paths check the P-sum
+    (:412-420)."""
+    n, r, m = 40, 24, 56
+    paths = [_mdbf_path(n, r, m, l, 10 * l + p) for p in range(2)]
+    x = np.random.default_rng(l).normal(size=(5, m)).astype(np.float32)
+    want = sum(_per_scale_forward(x, p) for p in paths)
+    got = od.mdbf_forward(x, paths, dtype="fp32")
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+    x16 = x.astype(np.float16)
+    paths16 = [{k: (v.astype(np.float16) if k.endswith("amp") else v) for k, v in p.items()} for p in paths]
+    want16 = sum(_per_scale_forward(x16, p) for p in paths16)
+    got16 = od.mdbf_forward(x16, paths16, dtype="fp16")
+    assert np.max(np.abs(got16 - want16)) / np.max(np.abs(want16)) < 1e-2
+
+
+def test_mdbf_planted_qu_qv_swap_is_caught(monkeypatch):
+    """A planted Q_U <-> Q_V swap in the oracle's factor construction (possible only for l > 1
+    to matter) must fail the per-scale comparison."""
+    real = od.mdbf_path_factors
+
+    def swapped(a_packed, a_shape, b_packed, b_shape, a_amp, b_amp, qu_amp, qv_amp, dtype="fp16"):
+        return real(a_packed, a_shape, b_packed, b_shape, a_amp, b_amp, qv_amp, qu_amp, dtype)
+
+    n, r, m, l = 40, 24, 56, 2
+    paths = [_mdbf_path(n, r, m, l, 77)]
+    x = np.random.default_rng(78).normal(size=(5, m)).astype(np.float32)
+    want = _per_scale_forward(x, paths[0])
+    assert np.max(np.abs(od.mdbf_forward(x, paths, dtype="fp32") - want)) / np.max(np.abs(want)) < 1e-5
+    monkeypatch.setattr(od, "mdbf_path_factors", swapped)
+    bad = od.mdbf_forward(x, paths, dtype="fp32")
+    assert np.max(np.abs(bad - want)) / np.max(np.abs(want)) > 1e-2
