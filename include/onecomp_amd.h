@@ -128,6 +128,22 @@ int oc_gptq_gemm(const void* x, int M, int K, int N, const void* packed, const u
                  const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
                  void* y, void* workspace, size_t ws_bytes, void* stream);
 
+/* Allocation-free variant of oc_gptq_gemm (no counterpart in the reference): for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  Same arguments, plans and results as oc_gptq_gemm, minus the workspace: the
+ * work buffer is the library's own per-GPU scratch array of oc_gptq_noalloc_scratch_bytes()
+ * (64 MiB) bytes, held until the process ends.  Calls that would need more (act-order x
+ * gathers of M * K * 2 bytes, split-K partial tiles) fail with OC_ERR_WORKSPACE.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race.  The current device must be the one `stream` belongs to.  No allocation, no memset, no
+ * host synchronisation. */
+int oc_gptq_gemm_noalloc(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
+                         const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
+                         void* y, void* stream);
+
+/* Bytes of the per-GPU scratch array oc_gptq_gemm_noalloc uses (host only). */
+size_t oc_gptq_noalloc_scratch_bytes(void);
+
 /* One part of a fused GPTQ module (e.g. q, k and v of qkv_proj): its repacked weights
  * (oc_gptq_prepare), act-order permutation or NULL, bias [N] or NULL, width, bits, group size. */
 typedef struct {

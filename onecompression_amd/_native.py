@@ -37,6 +37,8 @@ SIGNATURES = {
     "oc_gptq_describe_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_char_p, c_int]),
     "oc_gptq_gemm": (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P, P,
                              c_size_t, P]),
+    "oc_gptq_gemm_noalloc": (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P, P]),
+    "oc_gptq_noalloc_scratch_bytes": (c_size_t, []),
     "oc_gptq_grouped_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
     "oc_gptq_gemm_grouped": (c_int, [P, c_int, c_int, P, c_int, c_int, P, c_int, P, c_size_t, P]),
     "oc_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),

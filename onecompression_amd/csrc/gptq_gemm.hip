@@ -19,6 +19,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "gemm_core.h"
 #include "gptq_decode.h"
 #include "oc_common.h"
@@ -1785,6 +1787,59 @@ extern "C" int oc_gptq_gemm(const void* x, int M, int K, int N, const void* pack
                             void* y, void* workspace, size_t ws_bytes, void* stream) {
   return gptq_gemm_impl(x, M, K, N, packed, meta, perm, bits, group_size, act_dtype, bias, y, N, workspace,
                         ws_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of oc_gptq_gemm: the work buffer is this file's
+// device array `scratch` (kNoAllocScratch bytes per GPU, held until the
+// process ends).  Host code never passes the array's name to a kernel: its
+// device address is looked up once per device with hipGetSymbolAddress and
+// kept in g_scratch_ptr.  Every call on a GPU shares that GPU's array, so
+// calls that overlap on one GPU race.  No kernel of oc_gptq_gemm needs its
+// work buffer cleared (every byte read is written earlier in the same call).
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratch = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratch];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  OC_HIP(hipGetDevice(&dev));
+  OC_REQUIRE(dev >= 0 && dev < kMaxDevices, OC_ERR_INVALID, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    OC_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    OC_REQUIRE(p != nullptr, OC_ERR_HIP, "hipGetSymbolAddress returned a null address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" size_t oc_gptq_noalloc_scratch_bytes(void) { return kNoAllocScratch; }
+
+extern "C" int oc_gptq_gemm_noalloc(const void* x, int M, int K, int N, const void* packed, const uint32_t* meta,
+                                    const int32_t* perm, int bits, int group_size, int act_dtype, const void* bias,
+                                    void* y, void* stream) {
+  OC_REQUIRE(bits == 2 || bits == 3 || bits == 4 || bits == 8, OC_ERR_UNSUPPORTED, "unsupported bits=%d", bits);
+  OC_REQUIRE(M >= 0 && K > 0 && N > 0, OC_ERR_INVALID, "bad shape M=%d K=%d N=%d", M, K, N);
+  if (M == 0) return 0;
+  const size_t need = oc_gptq_workspace_bytes(M, K, N, bits, group_size, perm != nullptr);
+  OC_REQUIRE(need <= kNoAllocScratch, OC_ERR_WORKSPACE,
+             "this call needs %zu bytes of work buffer; the allocation-free entry point holds at most %zu "
+             "(use oc_gptq_gemm with a caller workspace)", need, kNoAllocScratch);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+  }
+  return gptq_gemm_impl(x, M, K, N, packed, meta, perm, bits, group_size, act_dtype, bias, y, N, ws,
+                        need > 0 ? kNoAllocScratch : 0, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -165,6 +165,33 @@ def gptq_gemm(x: torch.Tensor, prep: PreparedGPTQ, bias: Optional[torch.Tensor] 
     return out.reshape(*lead, n)
 
 
+def gptq_gemm_noalloc(x: torch.Tensor, prep: PreparedGPTQ, bias: Optional[torch.Tensor] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gptq_gemm through oc_gptq_gemm_noalloc: the library's per-GPU scratch array instead of a
+    workspace (nothing is allocated when ``out`` is given and x is contiguous)."""
+    dev = prep.packed.device
+    if x.dtype not in _DT:
+        raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
+    k, n = prep.in_features, prep.out_features
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} features, layer expects {k}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    _need(x2, "x", x.dtype, dev=dev)
+    m = x2.shape[0]
+    if bias is not None:
+        _need(bias, "bias", x.dtype, (n,), dev)
+    if out is None:
+        out = torch.empty((m, n), dtype=x.dtype, device=dev)
+    else:
+        _need(out, "out", x.dtype, (m, n), dev)
+    N.call("oc_gptq_gemm_noalloc", _ptr(x2), m, k, n, _ptr(prep.packed), _ptr(prep.meta), _ptr(prep.perm),
+           prep.bits, prep.group_size, _DT[x.dtype], _ptr(bias), _ptr(out), _stream(dev))
+    return out.reshape(*lead, n)
+
+
 class OcGptqPart(ctypes.Structure):
     _fields_ = [("packed", ctypes.c_void_p), ("meta", ctypes.c_void_p), ("perm", ctypes.c_void_p),
                 ("bias", ctypes.c_void_p), ("N", ctypes.c_int), ("bits", ctypes.c_int),
