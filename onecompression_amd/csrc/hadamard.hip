@@ -18,9 +18,15 @@
 //   Paley II (q prime, q = 1 mod 4, K = 2(q + 1)): H = A (x) C + B (x) I with
 //            C the symmetric conference matrix [[0, 1], [1, chi(j - i)]],
 //            A = [[1, 1], [1, -1]], B = [[1, -1], [-1, -1]];
-//   doubling: H_2K = [[1, 1], [1, -1]] (x) H_K.
-// chi is the quadratic character mod q.  Orders 52, 100, 156 and 172 (Paley
-// over GF(25) / GF(49) and other constructions) are not built.
+//   doubling: H_2K = [[1, 1], [1, -1]] (x) H_K;
+//   Williamson (K = 4q): H = [[A, B, C, D], [-B, A, -D, C], [-C, D, A, -B],
+//            [-D, -C, B, A]] with A..D symmetric q x q circulants,
+//            A^2 + B^2 + C^2 + D^2 = 4q I.  The reference's orders 52, 100,
+//            156 and 172 are Williamson matrices of this array; a symmetric
+//            circulant is fixed by the first (q + 1) / 2 entries of its first
+//            row, which kWill lists (the data that selects the reference's
+//            matrices among the Williamson quadruples of each order).
+// chi is the quadratic character mod q.
 //
 // One kernel, one workgroup per row: the length-L transforms in fp32 in LDS,
 // then u = FWHT / sqrt(n) rounded to the activation dtype and the H_K block
@@ -40,12 +46,50 @@ namespace {
 // Orders in the reference's search order (largest first), with how to build them.
 struct HadOrder {
   int K;
-  int kind;  // 1 Paley I, 2 Paley II, 3 doubling of the order K/2
+  int kind;  // 1 Paley I, 2 Paley II, 3 doubling of the order K/2, 4 Williamson (q = K/4)
   int q;
 };
-constexpr HadOrder kOrders[] = {{172, 0, 0}, {156, 0, 0}, {140, 1, 139}, {108, 1, 107}, {100, 0, 0},
-                                {76, 2, 37},  {68, 1, 67},  {60, 1, 59},   {52, 0, 0},    {44, 1, 43},
+constexpr HadOrder kOrders[] = {{172, 4, 43}, {156, 4, 39}, {140, 1, 139}, {108, 1, 107}, {100, 4, 25},
+                                {76, 2, 37},  {68, 1, 67},  {60, 1, 59},   {52, 4, 13},   {44, 1, 43},
                                 {40, 3, 0},   {36, 2, 17},  {28, 2, 13},   {20, 1, 19},   {12, 1, 11}};
+
+// Williamson generators: for each q, the first (q + 1) / 2 signs of the first
+// rows of A, B, C, D ('+' = 1).
+struct WillGen {
+  int q;
+  const char* half[4];
+};
+constexpr WillGen kWill[] = {
+    {13, {"+-+--++", "+---+++", "++-+--+", "+----+-"}},
+    {25, {"+-++++----++-", "+++-+++---+-+", "+-++-+++-++--", "+--++-+-+----"}},
+    {39, {"+++--+-+-----+--++--", "++++---+--++----+-+-", "+++--++-+---+-+--+--", "+---++-+-+-----+++-+"}},
+    {43, {"+---++--++++-+-+++-++-", "++-++++++----+-+--++-+", "+++-+-++--+-+-++++-+--",
+          "++---++++-+--+--++----"}},
+};
+
+bool build_williamson(int q, int8_t* H) {
+  const WillGen* g = nullptr;
+  for (const WillGen& w : kWill)
+    if (w.q == q) g = &w;
+  if (!g) return false;
+  int8_t row[4][64];
+  for (int b = 0; b < 4; ++b)
+    for (int j = 0; j <= q / 2; ++j) {
+      const int8_t v = g->half[b][j] == '+' ? 1 : -1;
+      row[b][j] = v;
+      row[b][(q - j) % q] = v;  // symmetric circulant: entry j equals entry q - j
+    }
+  // block (bi, bj) of the array is sign * X with X in {A, B, C, D} (indices 0..3)
+  static const int blk[4][4] = {{0, 1, 2, 3}, {1, 0, 3, 2}, {2, 3, 0, 1}, {3, 2, 1, 0}};
+  static const int sgn[4][4] = {{1, 1, 1, 1}, {-1, 1, -1, 1}, {-1, 1, 1, -1}, {-1, -1, 1, 1}};
+  const int K = 4 * q;
+  for (int bi = 0; bi < 4; ++bi)
+    for (int bj = 0; bj < 4; ++bj)
+      for (int i = 0; i < q; ++i)
+        for (int j = 0; j < q; ++j)
+          H[(bi * q + i) * K + bj * q + j] = (int8_t)(sgn[bi][bj] * row[blk[bi][bj]][((j - i) % q + q) % q]);
+  return true;
+}
 
 int quad_char(int a, int q) {
   a %= q;
@@ -100,6 +144,7 @@ bool build_order(int K, int8_t* H) {
       build_paley2(o.q, H);
       return true;
     }
+    if (o.kind == 4) return build_williamson(o.q, H);
     if (o.kind == 3) {
       const int h = K / 2;
       int8_t* S = (int8_t*)malloc((size_t)h * h);
@@ -426,7 +471,7 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
 // k_hadamard, with L / 16 workgroups per row instead of one.  Needs L >= 16
 // and y not overlapping x (workgroups of a row read all of it while others
 // store).
-constexpr int kHadMmMaxKT = 9;                      // K <= 144
+constexpr int kHadMmMaxKT = 11;                     // K <= 176
 constexpr int kHadMmUS = kHadMmMaxKT * 16 + 24;     // LDS row of the u tile (halves)
 constexpr int kHadMmMaxN = 32768;                   // row staged whole in LDS
 // LDS: block c of the row at c (L + 8) halves (the 16-B pad keeps the 16 lanes of a B read, one
@@ -560,7 +605,8 @@ extern "C" int oc_hadamard_block(int K, int8_t* out) {
     return 0;
   }
   OC_REQUIRE(build_order(K, out), OC_ERR_UNSUPPORTED,
-             "Hadamard block of order %d is not built (supported: 12, 20, 28, 36, 40, 44, 60, 68, 76, 108, 140)",
+             "no Hadamard block of order %d (the reference lists 12, 20, 28, 36, 40, 44, 52, 60, 68, 76, 100, 108, "
+             "140, 156, 172)",
              K);
   return 0;
 }
@@ -608,7 +654,7 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
       hipLaunchKernelGGL((k_hadamard_mm<KT_, false>), grid, dim3(256), mlds, st, (const uint16_t*)x, ld_x, n, Lh,   \
                          K, hadk, sc, (uint16_t*)y, ld_y);                                                      \
   }
-    OC_HM(1) OC_HM(2) OC_HM(3) OC_HM(4) OC_HM(5) OC_HM(6) OC_HM(7) OC_HM(8) OC_HM(9)
+    OC_HM(1) OC_HM(2) OC_HM(3) OC_HM(4) OC_HM(5) OC_HM(6) OC_HM(7) OC_HM(8) OC_HM(9) OC_HM(10) OC_HM(11)
 #undef OC_HM
     OC_HIP(hipGetLastError());
     return 0;

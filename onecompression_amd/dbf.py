@@ -51,17 +51,17 @@ def compute_mid_features(w_bit: float, in_features: int, out_features: int) -> i
     return min(min(in_features, out_features), mid)
 
 
-def _shard_id_to_index(shard_id: Any) -> int:
-    if shard_id is None:
-        return 0
-    if isinstance(shard_id, int):
-        return shard_id
-    if isinstance(shard_id, str):
-        mapping = {"q": 0, "k": 1, "v": 2}
-        if shard_id not in mapping:
-            raise ValueError(f"Unknown shard id: {shard_id}")
-        return mapping[shard_id]
-    raise TypeError(f"Unsupported shard id type: {type(shard_id)}")
+def _part_index(shard_id: Any) -> int:
+    """Which part of a fused DBF module a loader call fills: the whole parameter (None), a part
+    number, or the q/k/v letter of a fused qkv_proj."""
+    if shard_id is None or isinstance(shard_id, int):
+        return shard_id or 0
+    if not isinstance(shard_id, str):
+        raise TypeError(f"shard id must be None, an int or one of 'q', 'k', 'v'; got {type(shard_id)}")
+    letters = ("q", "k", "v")
+    if shard_id not in letters:
+        raise ValueError(f"Unknown shard id: {shard_id}")
+    return letters.index(shard_id)
 
 
 def _tp_size() -> int:
@@ -75,12 +75,9 @@ def _tp_size() -> int:
         return 1
 
 
-def _offsets(sizes: List[int]) -> List[int]:
-    out, c = [], 0
-    for s in sizes:
-        out.append(c)
-        c += s
-    return out
+def _starts(sizes: List[int]) -> List[int]:
+    """Start of each part when the parts lie back to back."""
+    return [sum(sizes[:i]) for i in range(len(sizes))]
 
 
 class DBFLinearMethod(LinearMethodBase):
@@ -93,65 +90,57 @@ class DBFLinearMethod(LinearMethodBase):
                        output_partition_sizes: List[int], input_size: int, output_size: int,
                        params_dtype: torch.dtype, **extra_weight_attrs):
         if _tp_size() != 1:
-            raise ValueError("DBF quantization currently supports only tensor_parallel_size=1.")
-        del params_dtype, output_size
-        part_count = len(output_partition_sizes)
-        in_features = input_size
+            raise ValueError("DBF layers run unsharded: tensor_parallel_size=1 is required.")
+        K = input_size
+        outs = list(output_partition_sizes)
+        n_parts = len(outs)
         mod_cfg = getattr(layer, "_dbf_mod_cfg", None)
         if mod_cfg is None:
-            logger.warning("DBF module config is missing on layer; defaulting bits=1.0.")
-            w_bit = 1.0
-        else:
-            w_bit = mod_cfg.get("bits", 0)
-        mids = [compute_mid_features(w_bit, in_features, n) for n in output_partition_sizes]
-        bp1_sizes = [(r * in_features + 7) // 8 for r in mids]
-        bp3_sizes = [(n * r + 7) // 8 for n, r in zip(output_partition_sizes, mids)]
-        meta = {
-            "part_count": part_count,
-            "in_features": in_features,
-            "out_sizes": list(output_partition_sizes),
-            "mid_sizes": mids,
-            "scaling2_offsets": _offsets(mids),
-            "scaling4_offsets": _offsets(list(output_partition_sizes)),
-            "bp1_offsets": _offsets(bp1_sizes),
-            "bp3_offsets": _offsets(bp3_sizes),
-            "bp1_sizes": bp1_sizes,
-            "bp3_sizes": bp3_sizes,
+            logger.warning("layer %s carries no DBF module config; assuming 1.0 bit per weight",
+                           getattr(layer, "prefix", "?"))
+        bits = 1.0 if mod_cfg is None else mod_cfg.get("bits", 0)
+        # per part p: rank r_p, and the bytes of its two packed sign factors (r_p x K and N_p x r_p)
+        ranks = [compute_mid_features(bits, K, n) for n in outs]
+        s2_bytes = [(r * K + 7) // 8 for r in ranks]
+        s1_bytes = [(n * r + 7) // 8 for n, r in zip(outs, ranks)]
+        layer._dbf_meta = {
+            "part_count": n_parts, "in_features": K, "out_sizes": outs, "mid_sizes": ranks,
+            "scaling2_offsets": _starts(ranks), "scaling4_offsets": _starts(outs),
+            "bp1_offsets": _starts(s2_bytes), "bp3_offsets": _starts(s1_bytes),
+            "bp1_sizes": s2_bytes, "bp3_sizes": s1_bytes,
         }
-        layer._dbf_meta = meta
-        extra_weight_attrs = dict(extra_weight_attrs)
-        extra_weight_attrs.pop("weight_loader", None)
+        attrs = {k: v for k, v in extra_weight_attrs.items() if k != "weight_loader"}
 
-        def make_loader(kind: str, offsets: List[int], sizes: List[int]):
-            def _loader(param: Parameter, loaded_weight: torch.Tensor, shard_id: Any = None):
-                idx = _shard_id_to_index(shard_id)
-                if part_count > 1 and shard_id is None:
-                    raise ValueError(f"DBF expects shard_id for fused module parameter {kind}.")
-                if kind == "scaling0":
-                    if param.data.ndim == 2:
-                        param.data[idx].copy_(loaded_weight)
-                    else:
-                        param.data.copy_(loaded_weight)
-                    return
-                param.data.narrow(0, offsets[idx], sizes[idx]).copy_(loaded_weight)
+        # Checkpoint parameters: name -> (storage, per-part sizes along dim 0, or None for scaling0,
+        # which holds one row per part when the module is fused).
+        stacked_s0 = n_parts > 1
+        params = {
+            "scaling0": (torch.empty((n_parts, K) if stacked_s0 else (K,), dtype=torch.float16), None),
+            "scaling2": (torch.empty(sum(ranks), dtype=torch.float16), ranks),
+            "scaling4": (torch.empty(sum(outs), dtype=torch.float16), outs),
+            "bp1": (torch.empty(sum(s2_bytes), dtype=torch.uint8), s2_bytes),
+            "bp3": (torch.empty(sum(s1_bytes), dtype=torch.uint8), s1_bytes),
+        }
 
-            return _loader
+        def loader_for(name: str, sizes: Optional[List[int]]):
+            starts = None if sizes is None else _starts(sizes)
 
-        def reg(name, tensor, loader):
-            p = Parameter(tensor, requires_grad=False)
-            set_weight_attrs(p, {**extra_weight_attrs, "weight_loader": loader})
-            layer.register_parameter(name, p)
+            def load(param: Parameter, loaded_weight: torch.Tensor, shard_id: Any = None):
+                if shard_id is None and n_parts > 1:
+                    raise ValueError(f"DBF parameter {name} of a fused module is loaded per part; "
+                                     f"a shard_id is required.")
+                p = _part_index(shard_id)
+                if sizes is None:  # scaling0: its row of the stack, or the whole vector
+                    (param.data[p] if stacked_s0 else param.data).copy_(loaded_weight)
+                else:
+                    param.data[starts[p]:starts[p] + sizes[p]].copy_(loaded_weight)
 
-        s0_shape = (part_count, in_features) if part_count > 1 else (in_features,)
-        reg("scaling0", torch.empty(s0_shape, dtype=torch.float16), make_loader("scaling0", [], []))
-        reg("scaling2", torch.empty(sum(mids), dtype=torch.float16),
-            make_loader("scaling2", meta["scaling2_offsets"], mids))
-        reg("scaling4", torch.empty(sum(output_partition_sizes), dtype=torch.float16),
-            make_loader("scaling4", meta["scaling4_offsets"], list(output_partition_sizes)))
-        reg("bp1", torch.empty(sum(bp1_sizes), dtype=torch.uint8),
-            make_loader("bp1", meta["bp1_offsets"], bp1_sizes))
-        reg("bp3", torch.empty(sum(bp3_sizes), dtype=torch.uint8),
-            make_loader("bp3", meta["bp3_offsets"], bp3_sizes))
+            return load
+
+        for name, (storage, sizes) in params.items():
+            prm = Parameter(storage, requires_grad=False)
+            set_weight_attrs(prm, {**attrs, "weight_loader": loader_for(name, sizes)})
+            layer.register_parameter(name, prm)
 
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
         if getattr(layer, "_dbf_initialized", False):

@@ -11,9 +11,9 @@ Drop-in for vllm_plugins/gptq (registered as ``"mixed_gptq"``):
 - Where the reference hands 4/8-bit symmetric layers to vLLM's Marlin kernel
   and everything else to vLLM's Exllama kernel (:332-353,
   vllm_plugins/gptq/constants.py:12-31), every GPTQ layer here goes to
-  :class:`GPTQLinearMethod`, one HIP kernel family for 2/3/4/8 bits with or
+  :class:`MixedGPTQLinearMethod`, one HIP kernel family for 2/3/4/8 bits with or
   without act-order.
-- :class:`GPTQLinearMethod` registers the checkpoint tensors under the same
+- :class:`MixedGPTQLinearMethod` registers the checkpoint tensors under the same
   names and shapes (``qweight`` [K*b/32, N] int32, ``qzeros`` [G, N*b/32]
   int32, ``scales`` [G, N], ``g_idx`` [K] int32), repacks them once in
   ``process_weights_after_loading`` and runs ``apply`` as one C-ABI call.
@@ -59,7 +59,7 @@ _MOE_EXPERT_CFG_RE = re.compile(r"(?:^|\.)experts\.\d+\.")
 
 
 class GPTQLayerConfig:
-    """Per-layer GPTQ parameters handed to :class:`GPTQLinearMethod`."""
+    """Per-layer GPTQ parameters handed to :class:`MixedGPTQLinearMethod`."""
 
     def __init__(self, bits: int, group_size: int, desc_act: bool, sym: bool,
                  checkpoint_format: str):
@@ -100,8 +100,14 @@ def _shard_index(shard_id: Any, n_parts: int) -> int:
     raise ValueError(f"Unknown shard id: {shard_id}")
 
 
-class GPTQLinearMethod(LinearMethodBase):
-    """Linear method for one GPTQ layer (replaces vLLM's GPTQ/Marlin methods)."""
+class MixedGPTQLinearMethod(LinearMethodBase):
+    """Linear method for one GPTQ layer (replaces vLLM's GPTQ/Marlin methods).
+
+    vLLM chooses a layer's weight loader by the method's class name (names in its
+    WEIGHT_LOADER_V2_SUPPORTED list get the v2 loader, which needs vLLM's parameter classes).
+    This method registers plain Parameters with the v1 attributes (input_dim, output_dim,
+    packed_dim, pack_factor), so its name stays outside that list -- vLLM's own
+    ``GPTQLinearMethod`` is in it."""
 
     def __init__(self, quant_config: GPTQLayerConfig):
         self.quant_config = quant_config
@@ -164,7 +170,7 @@ class GPTQLinearMethod(LinearMethodBase):
         cfg = self.quant_config
         dev = layer.qweight.device
         if dev.type != "cuda":
-            raise RuntimeError("GPTQLinearMethod needs the layer on a HIP device before "
+            raise RuntimeError("MixedGPTQLinearMethod needs the layer on a HIP device before "
                                "process_weights_after_loading")
         scales = layer.scales.data
         if scales.dtype != torch.float16:
@@ -435,27 +441,21 @@ class MixedGPTQConfig(QuantizationConfig):
                  lm_head_quantized=False, checkpoint_format="gptq_v2",
                  rotation_metadata: Optional[RotationMetadata] = None, fused_mixed_bits: bool = False):
         super().__init__()
-        # Extension (off by default, as in the reference): serve fused modules whose shards
-        # differ in bits or group size instead of raising ValueError.
-        self.fused_mixed_bits = bool(fused_mixed_bits)
-        self.quantization_bits = quantization_bits
-        self.group_size = group_size
-        self.desc_act = desc_act
-        self.sym = sym
+        self.quantization_bits = quantization_bits  # one {module name: entry} dict per decoder layer
+        self.group_size, self.desc_act, self.sym = group_size, desc_act, sym
         self.lm_head_quantized = lm_head_quantized
         self.checkpoint_format = checkpoint_format
-        self.rotation_metadata = rotation_metadata if rotation_metadata is not None else RotationMetadata()
-        bits, methods = set(), set()
-        for layer_cfg in quantization_bits:
-            for mod_cfg in layer_cfg.values():
-                bits.add(mod_cfg.get("bits", 0))
-                methods.add(mod_cfg.get("method", "gptq"))
-        logger.info("MixedGPTQConfig: %d layers, bits=%s, methods=%s", len(quantization_bits),
-                    sorted(bits), sorted(methods))
+        self.rotation_metadata = rotation_metadata or RotationMetadata()
+        # This build's extension, off unless the config asks for it: serve fused modules whose
+        # shards differ in bits or group size instead of raising ValueError.
+        self.fused_mixed_bits = bool(fused_mixed_bits)
+        entries = [e for per_layer in quantization_bits for e in per_layer.values()]
+        logger.info("mixed_gptq over %d decoder layers: bit widths %s, methods %s", len(quantization_bits),
+                    sorted({e.get("bits", 0) for e in entries}), sorted({e.get("method", "gptq") for e in entries}))
 
     def __repr__(self):
-        return (f"MixedGPTQConfig(layers={len(self.quantization_bits)}, "
-                f"group_size={self.group_size}, desc_act={self.desc_act})")
+        return (f"MixedGPTQConfig(num_layers={len(self.quantization_bits)}, group_size={self.group_size}, "
+                f"desc_act={self.desc_act}, checkpoint_format={self.checkpoint_format!r})")
 
     @classmethod
     def get_name(cls) -> str:
@@ -490,15 +490,18 @@ class MixedGPTQConfig(QuantizationConfig):
     def maybe_update_config(self, model_name, hf_config=None, revision=None):
         """No-op: per-module dispatch comes from ``quantization_bits`` (vllm_plugin.py:213-218)."""
 
-    def resolve_group_size(self, mod_cfg: Optional[Dict]) -> int:
-        """Per-module direct > ``params`` > global (vllm_plugin.py:165-173)."""
-        if mod_cfg is not None:
-            if mod_cfg.get("group_size") is not None:
-                return mod_cfg["group_size"]
-            extra = mod_cfg.get("params", {})
-            if isinstance(extra, dict) and extra.get("group_size") is not None:
-                return extra["group_size"]
+    def _resolve_group_size(self, mod_cfg: Optional[Dict]) -> int:
+        """Group size of one module entry: the entry's own ``group_size``, else the one in its
+        ``params`` dict, else the config-wide value (vllm_plugin.py:165-173)."""
+        if mod_cfg is None:
+            return self.group_size
+        nested = mod_cfg.get("params")
+        for candidate in (mod_cfg.get("group_size"), nested.get("group_size") if isinstance(nested, dict) else None):
+            if candidate is not None:
+                return candidate
         return self.group_size
+
+    resolve_group_size = _resolve_group_size
 
     def _mixed_fused_method(self, layer_idx: int, suffix: str, prefix: str):
         """MixedFusedGPTQLinearMethod when enabled and every shard is a GPTQ entry, else None."""
@@ -522,19 +525,19 @@ class MixedGPTQConfig(QuantizationConfig):
                                           metadata=self.rotation_metadata)
 
     def _lookup_moe_expert_config(self, layer_idx: int) -> Optional[Dict[str, Any]]:
-        """A representative per-expert GPTQ entry of a MoE layer: gate_proj first, then up, down,
-        then any expert projection (vllm_plugin.py:220-239; all experts share bits/group size)."""
-        if layer_idx >= len(self.quantization_bits):
+        """The entry that configures a MoE layer's experts (all experts share bits and group size,
+        vllm_plugin.py:220-239): among the layer's ``experts.<i>.`` entries, the first gate_proj,
+        else the first up_proj, else the first down_proj, else the first of any kind."""
+        if not 0 <= layer_idx < len(self.quantization_bits):
             return None
-        layer_cfg = self.quantization_bits[layer_idx]
-        for suffix in (".gate_proj", ".up_proj", ".down_proj"):
-            for name, cfg in layer_cfg.items():
-                if _MOE_EXPERT_CFG_RE.search(name) and name.endswith(suffix):
-                    return cfg
-        for name, cfg in layer_cfg.items():
-            if _MOE_EXPERT_CFG_RE.search(name):
-                return cfg
-        return None
+        preference = (".gate_proj", ".up_proj", ".down_proj")
+
+        def rank(name: str) -> int:
+            return next((i for i, suffix in enumerate(preference) if name.endswith(suffix)), len(preference))
+
+        experts = [(rank(n), i, c) for i, (n, c) in enumerate(self.quantization_bits[layer_idx].items())
+                   if _MOE_EXPERT_CFG_RE.search(n)]
+        return min(experts, key=lambda t: t[:2])[2] if experts else None
 
     def _get_moe_quant_method(self, layer: torch.nn.Module, prefix: str):
         """GPTQMoEMethod for a FusedMoE layer with per-expert GPTQ entries, else None (unquantized
@@ -575,7 +578,7 @@ class MixedGPTQConfig(QuantizationConfig):
         if method == "gptq" and int(bits) in SUPPORTED_BITS:
             cfg = GPTQLayerConfig(int(bits), self.resolve_group_size(mod_cfg), self.desc_act,
                                   bool(self.sym), self.checkpoint_format)
-            return maybe_wrap_rotation_method(GPTQLinearMethod(cfg), prefix=prefix,
+            return maybe_wrap_rotation_method(MixedGPTQLinearMethod(cfg), prefix=prefix,
                                               metadata=self.rotation_metadata)
         logger.warning("mixed_gptq: unsupported method=%s bits=%s at %s, falling back to unquantized",
                        method, bits, prefix)

@@ -36,14 +36,13 @@ from . import dbf_ops, ops
 
 
 def _normalize_wbits(wbits) -> int:
-    """Integral wbits as a builtin int (gptq_layer.py:214-227)."""
-    if isinstance(wbits, bool):
+    """wbits as a builtin int.  Integers (bool excluded) and integral floats are accepted; any other
+    value raises ValueError (the contract of gptq_layer.py:214-227)."""
+    integral = (isinstance(wbits, int) and not isinstance(wbits, bool)) or \
+        (isinstance(wbits, float) and wbits.is_integer())
+    if not integral:
         raise ValueError(f"wbits must be an integer value, got {wbits!r}.")
-    if isinstance(wbits, int):
-        return int(wbits)
-    if isinstance(wbits, float) and wbits.is_integer():
-        return int(wbits)
-    raise ValueError(f"wbits must be an integer value, got {wbits!r}.")
+    return int(wbits)
 
 
 def _stamp(tensors) -> tuple:
@@ -65,40 +64,29 @@ class GPTQLinear(nn.Module):
         """gptq_layer.py:630-714: buffers from a layer state dict (zeros when ``empty``)."""
         self = cls.__new__(cls)
         nn.Module.__init__(self)
-        wbits = _normalize_wbits(wbits)
         self.in_features, self.out_features = in_features, out_features
-        self.wbits, self.groupsize, self.actorder = wbits, groupsize, actorder
+        self.wbits, self.groupsize, self.actorder = _normalize_wbits(wbits), groupsize, actorder
         self.checkpoint_format = checkpoint_format
-        self._weight_is_packed = wbits != 1
-
-        def _t(k):
-            t = layer_state_dict[k]
-            return torch.zeros_like(t) if empty else t
-
-        dev = layer_state_dict["qweight"].device
-        self.register_buffer("qweight", _t("qweight"))
-        self.register_buffer("scales", _t("scales"))
-        self.register_buffer("qzeros", _t("qzeros"))
-        g_idx = layer_state_dict.get("g_idx")
-        if g_idx is not None:
-            self.register_buffer("g_idx", torch.zeros_like(g_idx) if empty else g_idx)
-        elif groupsize != -1:
-            self.register_buffer("g_idx", torch.arange(in_features, dtype=torch.int32, device=dev) // groupsize)
-        else:
-            self.register_buffer("g_idx", torch.zeros(in_features, dtype=torch.int32, device=dev))
-        perm = layer_state_dict.get("perm")
-        if perm is not None:
-            self.register_buffer("perm", torch.zeros_like(perm) if empty else perm)
-        else:
-            self.perm = None
-        bias = layer_state_dict.get("bias")
-        if bias is not None:
-            self.register_buffer("bias", torch.zeros_like(bias) if empty else bias)
-        else:
-            self.bias = None
+        self._weight_is_packed = self.wbits != 1  # 1-bit checkpoints are stored unpacked
         self.using_gemlite = False
         self._prep = None
         self._prep_stamp = None
+
+        missing = [k for k in ("qweight", "scales", "qzeros") if k not in layer_state_dict]
+        if missing:
+            raise KeyError(f"GPTQ layer state is missing {missing}")
+        take = {k: layer_state_dict[k] for k in ("qweight", "scales", "qzeros", "g_idx", "perm", "bias")
+                if layer_state_dict.get(k) is not None}
+        if empty:  # "replace, then load_state_dict": same shapes and dtypes, zero contents
+            take = {k: torch.zeros_like(t) for k, t in take.items()}
+        if "g_idx" not in take:  # no act-order tensor saved: the sequential groups k // groupsize
+            k = torch.arange(in_features, dtype=torch.int32, device=take["qweight"].device)
+            take["g_idx"] = k // groupsize if groupsize != -1 else torch.zeros_like(k)
+        for key in ("qweight", "scales", "qzeros", "g_idx", "perm", "bias"):
+            if key in take:
+                self.register_buffer(key, take[key])
+            else:
+                setattr(self, key, None)
         return self
 
     def _prepared(self) -> ops.PreparedGPTQ:

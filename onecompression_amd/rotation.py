@@ -24,6 +24,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Any, Dict, Optional
 
+from .vllm_compat import LinearMethodBase, WEIGHT_LOADER_V2_SUPPORTED, register_weight_loader_v2_supported_method
+
 
 def is_online_hadamard_target(name: str) -> bool:
     """Dense ``mlp.down_proj`` layers receive the online Hadamard."""
@@ -69,8 +71,12 @@ def make_hadamard_forward_pre_hook(*, fp32_had: bool):
     return hook
 
 
-class RotatedLinearMethod:
-    """Linear-method wrapper that transforms the layer input online (rotation.py:146-228)."""
+class RotatedLinearMethod(LinearMethodBase):
+    """Linear-method wrapper that transforms the layer input online (rotation.py:146-228).
+
+    Not on vLLM's v2 weight-loader list: it wraps base methods whose params take the v1 loader
+    (vLLM picks the loader by the wrapper's class name).  :class:`RotatedLinearMethodV2` is the
+    listed twin for v2-native bases."""
 
     def __init__(self, base_method, *, fp32_had: bool):
         self.base_method = base_method
@@ -107,8 +113,23 @@ class RotatedLinearMethod:
         return getattr(self.base_method, name)
 
 
+@register_weight_loader_v2_supported_method
+class RotatedLinearMethodV2(RotatedLinearMethod):
+    """The wrapper for base methods on vLLM's v2 weight-loader list (rotation.py:232-239)."""
+
+
+def _takes_v2_loader(method) -> bool:
+    """Whether vLLM would give ``method``'s layer the v2 weight loader (by class name); with no
+    inspectable list, assume v2, as the reference does (rotation.py:126-144)."""
+    if WEIGHT_LOADER_V2_SUPPORTED is None:
+        return True
+    return type(method).__name__ in WEIGHT_LOADER_V2_SUPPORTED
+
+
 def maybe_wrap_rotation_method(method, *, prefix: str, metadata: RotationMetadata):
-    """``method`` unchanged, or wrapped with the online Hadamard for rotated down_proj layers."""
+    """``method`` unchanged, or wrapped with the online Hadamard for rotated down_proj layers; the
+    wrapper keeps the base method's v1/v2 loader choice (rotation.py:242-261)."""
     if not metadata.requires_hadamard(prefix):
         return method
-    return RotatedLinearMethod(method, fp32_had=metadata.fp32_had)
+    cls = RotatedLinearMethodV2 if _takes_v2_loader(method) else RotatedLinearMethod
+    return cls(method, fp32_had=metadata.fp32_had)

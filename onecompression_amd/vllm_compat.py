@@ -33,6 +33,26 @@ try:  # pragma: no cover - exercised only where vLLM is installed
         from vllm.model_executor.layers.fused_moe import FusedMoE  # type: ignore
     except Exception:  # noqa: BLE001
         FusedMoE = None
+    try:
+        from vllm.model_executor.layers.linear import WEIGHT_LOADER_V2_SUPPORTED  # type: ignore
+    except Exception:  # noqa: BLE001
+        WEIGHT_LOADER_V2_SUPPORTED = None
+    try:
+        from vllm.model_executor.layers.linear import (  # type: ignore
+            register_weight_loader_v2_supported_method as _vllm_register_v2,
+        )
+    except Exception:  # noqa: BLE001
+        _vllm_register_v2 = None
+
+    def register_weight_loader_v2_supported_method(cls):
+        """Put ``cls``'s name on vLLM's v2 weight-loader list (the registry function when the
+        installed vLLM has one, else the list itself)."""
+        if _vllm_register_v2 is not None:
+            return _vllm_register_v2(cls)
+        if WEIGHT_LOADER_V2_SUPPORTED is not None and cls.__name__ not in WEIGHT_LOADER_V2_SUPPORTED:
+            WEIGHT_LOADER_V2_SUPPORTED.append(cls.__name__)
+        return cls
+
     HAS_VLLM = True
 except Exception:  # noqa: BLE001 - any import failure means "no vLLM"
     HAS_VLLM = False
@@ -81,10 +101,44 @@ except Exception:  # noqa: BLE001 - any import failure means "no vLLM"
         def get_quant_method(self, layer: torch.nn.Module, prefix: str):
             raise NotImplementedError
 
+    # vLLM hands a linear layer's params the v2 weight loader when the quant method's class name
+    # is on this list (LinearBase.__init__), else the v1 loader.  The names below are the vLLM
+    # methods this package meets or replaces; vLLM's own GPTQ method is among them.
+    WEIGHT_LOADER_V2_SUPPORTED: List[str] = [
+        "UnquantizedLinearMethod", "GPTQLinearMethod", "GPTQMarlinLinearMethod", "AWQLinearMethod",
+        "AWQMarlinLinearMethod", "MarlinLinearMethod", "Fp8LinearMethod", "CompressedTensorsLinearMethod",
+    ]
+
+    def register_weight_loader_v2_supported_method(cls):
+        if cls.__name__ not in WEIGHT_LOADER_V2_SUPPORTED:
+            WEIGHT_LOADER_V2_SUPPORTED.append(cls.__name__)
+        return cls
+
+    def _part_slot(loaded_shard_id: Any, n_parts: int) -> int:
+        if isinstance(loaded_shard_id, int):
+            return loaded_shard_id
+        letters = ("q", "k", "v")[:n_parts]
+        if loaded_shard_id not in letters:
+            raise ValueError(f"unknown shard id {loaded_shard_id!r}")
+        return letters.index(loaded_shard_id)
+
+    class _V2Parameter(torch.nn.Parameter):
+        """A parameter that loads itself, as vLLM's v2 parameter classes do."""
+
+        def load_column_parallel_weight(self, loaded_weight: torch.Tensor) -> None:
+            self.data.copy_(loaded_weight)
+
+        def load_merged_column_weight(self, loaded_weight: torch.Tensor, shard_offset: int,
+                                      shard_size: int) -> None:
+            self.data.narrow(self.output_dim, shard_offset, shard_size).copy_(loaded_weight)
+
     class LinearBase(torch.nn.Module):
         """Minimal linear layer in vLLM's style: the quant method owns the params.
 
-        ``output_partition_sizes`` lists the fused parts (e.g. q, k, v).
+        ``output_partition_sizes`` lists the fused parts (e.g. q, k, v).  As in vLLM, the weight
+        loader handed to ``create_weights`` is chosen by the quant method's class name: v2 when
+        it is on ``WEIGHT_LOADER_V2_SUPPORTED`` (the param must then load itself), else v1
+        (driven by the param's ``output_dim`` / ``packed_dim`` / ``pack_factor`` attributes).
         """
 
         def __init__(self, input_size: int, output_size: int, bias: bool = False,
@@ -103,24 +157,54 @@ except Exception:  # noqa: BLE001 - any import failure means "no vLLM"
                 self.quant_method = quant_config.get_quant_method(self, prefix)
             if self.quant_method is None:
                 self.quant_method = UnquantizedLinearMethod()
+            v2 = self.quant_method.__class__.__name__ in WEIGHT_LOADER_V2_SUPPORTED
+            self.loader_version = 2 if v2 else 1
             self.quant_method.create_weights(self, input_size, self.output_partition_sizes,
-                                             input_size, output_size, params_dtype)
+                                             input_size, output_size, params_dtype,
+                                             weight_loader=self.weight_loader_v2 if v2 else self.weight_loader)
             if bias:
                 self.bias = torch.nn.Parameter(torch.zeros(output_size, dtype=params_dtype),
                                                requires_grad=False)
             else:
                 self.register_parameter("bias", None)
 
+        def _shard_range(self, param, loaded_shard_id):
+            """Offset and size of a fused part along the param's output dim (in packed units when
+            the param is packed along it)."""
+            sizes = self.output_partition_sizes
+            i = _part_slot(loaded_shard_id, len(sizes))
+            off, size = sum(sizes[:i]), sizes[i]
+            if getattr(param, "packed_dim", None) == param.output_dim:
+                off, size = off // param.pack_factor, size // param.pack_factor
+            return int(off), int(size)
+
+        def weight_loader(self, param, loaded_weight: torch.Tensor, loaded_shard_id: Any = None):
+            """v1: the whole tensor, or one fused part placed along ``param.output_dim``."""
+            out_dim = getattr(param, "output_dim", None)
+            if loaded_shard_id is None or out_dim is None or len(self.output_partition_sizes) == 1:
+                param.data.copy_(loaded_weight)
+                return
+            off, size = self._shard_range(param, loaded_shard_id)
+            param.data.narrow(out_dim, off, size).copy_(loaded_weight)
+
+        def weight_loader_v2(self, param, loaded_weight: torch.Tensor, loaded_shard_id: Any = None):
+            """v2: the parameter loads itself (a plain Parameter has no such methods and fails)."""
+            if loaded_shard_id is None or len(self.output_partition_sizes) == 1:
+                param.load_column_parallel_weight(loaded_weight=loaded_weight)
+                return
+            off, size = self._shard_range(param, loaded_shard_id)
+            param.load_merged_column_weight(loaded_weight=loaded_weight, shard_offset=off, shard_size=size)
+
         def forward(self, x: torch.Tensor) -> torch.Tensor:
             return self.quant_method.apply(self, x, self.bias)
 
     class UnquantizedLinearMethod(LinearMethodBase):
-        """Stand-in for vllm...linear.UnquantizedLinearMethod (dense F.linear)."""
+        """Stand-in for vllm...linear.UnquantizedLinearMethod (dense F.linear; v2-native params)."""
 
         def create_weights(self, layer, input_size_per_partition, output_partition_sizes,
                            input_size, output_size, params_dtype, **extra_weight_attrs):
-            w = torch.nn.Parameter(torch.empty(sum(output_partition_sizes), input_size_per_partition,
-                                               dtype=params_dtype), requires_grad=False)
+            w = _V2Parameter(torch.empty(sum(output_partition_sizes), input_size_per_partition,
+                                         dtype=params_dtype), requires_grad=False)
             set_weight_attrs(w, {"input_dim": 1, "output_dim": 0, **extra_weight_attrs})
             layer.register_parameter("weight", w)
 

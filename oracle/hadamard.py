@@ -7,10 +7,10 @@ module, as the checker.  The product path is onecompression_amd/csrc/hadamard.hi
   largest listed K dividing n with n / K a power of two; n itself a power of
   two gives K = 1).
 - ``hadamard_block``: the K x K matrices, built from the classical
-  constructions (Paley I, Paley II, Sylvester doubling) instead of the
-  reference's literal tables.  Pinned: tests compare the SHA-256 of each
-  construction with tests/golden/hadamard_digests.json, written from the
-  reference's tables; orders 52, 100, 156, 172 are not constructed.
+  constructions (Paley I, Paley II, Sylvester doubling, the Williamson array
+  for 52, 100, 156, 172) instead of the reference's literal tables.  Pinned:
+  tests compare the SHA-256 of each construction with
+  tests/golden/hadamard_digests.json, written from the reference's tables.
 - ``fwht``: the unnormalised natural-order transform of
   hadamard_utils.py:26-44 (butterfly (a, b) -> (a + b, a - b) on blocks of
   2m).  Pinned by the closed form H[i, j] = (-1)^popcount(i & j).
@@ -23,9 +23,19 @@ from __future__ import annotations
 import numpy as np
 
 # (K, construction, q) in the reference's search order (hadamard_utils.py:93-172)
-ORDERS = [(172, None, 0), (156, None, 0), (140, "paley1", 139), (108, "paley1", 107), (100, None, 0),
-          (76, "paley2", 37), (68, "paley1", 67), (60, "paley1", 59), (52, None, 0), (44, "paley1", 43),
-          (40, "double", 20), (36, "paley2", 17), (28, "paley2", 13), (20, "paley1", 19), (12, "paley1", 11)]
+ORDERS = [(172, "williamson", 43), (156, "williamson", 39), (140, "paley1", 139), (108, "paley1", 107),
+          (100, "williamson", 25), (76, "paley2", 37), (68, "paley1", 67), (60, "paley1", 59),
+          (52, "williamson", 13), (44, "paley1", 43), (40, "double", 20), (36, "paley2", 17),
+          (28, "paley2", 13), (20, "paley1", 19), (12, "paley1", 11)]
+
+# Williamson generators per q: the first (q + 1) / 2 signs of the first rows of the symmetric
+# circulants A, B, C, D (the data that singles out the reference's matrices of orders 4q).
+WILLIAMSON = {
+    13: ("+-+--++", "+---+++", "++-+--+", "+----+-"),
+    25: ("+-++++----++-", "+++-+++---+-+", "+-++-+++-++--", "+--++-+-+----"),
+    39: ("+++--+-+-----+--++--", "++++---+--++----+-+-", "+++--++-+---+-+--+--", "+---++-+-+-----+++-+"),
+    43: ("+---++--++++-+-+++-++-", "++-++++++----+-+--++-+", "+++-+-++--+-+-++++-+--", "++---++++-+--+--++----"),
+}
 
 
 def is_pow2(n: int) -> bool:
@@ -77,6 +87,20 @@ def paley2(q: int) -> np.ndarray:
     return np.kron(A, C) + np.kron(B, np.eye(q + 1, dtype=np.int64))
 
 
+def symmetric_circulant(half: str, q: int) -> np.ndarray:
+    """q x q circulant X[i, j] = x[(j - i) mod q] with x[j] = x[q - j] given by its first half."""
+    h = np.array([1 if c == "+" else -1 for c in half], dtype=np.int64)
+    x = np.concatenate([h, h[1:q - len(h) + 1][::-1]])
+    idx = (np.arange(q)[None, :] - np.arange(q)[:, None]) % q
+    return x[idx]
+
+
+def williamson(q: int) -> np.ndarray:
+    """Order 4q: [[A, B, C, D], [-B, A, -D, C], [-C, D, A, -B], [-D, -C, B, A]]."""
+    A, B, C, D = (symmetric_circulant(h, q) for h in WILLIAMSON[q])
+    return np.block([[A, B, C, D], [-B, A, -D, C], [-C, D, A, -B], [-D, -C, B, A]])
+
+
 def hadamard_block(K: int) -> np.ndarray:
     if K == 1:
         return np.ones((1, 1), dtype=np.int64)
@@ -89,6 +113,8 @@ def hadamard_block(K: int) -> np.ndarray:
             return paley2(q)
         if how == "double":
             return np.kron(np.array([[1, 1], [1, -1]]), hadamard_block(q))
+        if how == "williamson":
+            return williamson(q)
         raise NotImplementedError(f"Hadamard order {K} is not constructed")
     raise ValueError(f"no Hadamard order {K}")
 

@@ -22,7 +22,8 @@ def _f32(t, dtype):
 
 
 @pytest.mark.parametrize("n", [14336, 12288, 17408, 4096, 24, 320, 2 * 140, 20, 4, 1, 32768, 27648, 28672,
-                               2240, 2304, 3840, 2432])  # the last four: blocks of 140, 36, 60, 76 (L >= 16)
+                               2240, 2304, 3840, 2432,  # blocks of 140, 36, 60, 76 (L >= 16)
+                               11008, 9984, 25600, 6656, 832, 2752, 2496])  # Williamson 172, 156, 100, 52 (+ L = 16)
 @pytest.mark.parametrize("m", [1, 3, 64])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_hadamard_matches_oracle(dev, n, m, dtype):

@@ -42,10 +42,30 @@ def test_planted_mistake_is_caught():
     assert _digest(H) != digests["12"]
 
 
-@pytest.mark.parametrize("K", [52, 100, 156, 172])
-def test_unbuilt_orders_raise(K):
-    with pytest.raises(NotImplementedError):
-        oh.hadamard_block(K)
+def test_every_reference_order_is_built():
+    with open(GOLDEN) as f:
+        digests = json.load(f)["digests"]
+    assert sorted(BUILT) == sorted(int(k) for k in digests)
+
+
+def test_williamson_planted_mistake_is_caught():
+    """The Williamson array with the roles of B and C exchanged in the second block row is no
+    longer the reference's matrix (and no longer orthogonal)."""
+    with open(GOLDEN) as f:
+        digests = json.load(f)["digests"]
+    q = 13
+    A, B, C, D = (oh.symmetric_circulant(h, q) for h in oh.WILLIAMSON[q])
+    H = np.block([[A, B, C, D], [-C, A, -D, B], [-B, D, A, -C], [-D, -C, B, A]])
+    assert _digest(H) != digests["52"]
+    good = oh.williamson(q)
+    assert np.array_equal(good @ good.T, 52 * np.eye(52, dtype=np.int64))
+
+
+def test_symmetric_circulant_closed_form():
+    X = oh.symmetric_circulant("+--+", 7)
+    assert np.array_equal(X, X.T)
+    assert X[0].tolist() == [1, -1, -1, 1, 1, -1, -1]
+    assert all(np.array_equal(np.roll(X[0], i), X[i]) for i in range(7))
 
 
 def test_pick_order():
@@ -90,9 +110,9 @@ def test_c_abi_blocks_and_orders_match_oracle():
         buf = (ctypes.c_int8 * (K * K))()
         assert lib.oc_hadamard_block(K, buf) == 0
         assert np.array_equal(np.array(list(buf), dtype=np.int64).reshape(K, K), oh.hadamard_block(K))
-    for K in (52, 100, 156, 172):
+    for K in (24, 48, 88):
         buf = (ctypes.c_int8 * (K * K))()
         assert lib.oc_hadamard_block(K, buf) == N.OC_ERR_UNSUPPORTED
-    for n in (14336, 12288, 17408, 11008, 4096, 640):
+    for n in (14336, 12288, 17408, 11008, 4096, 640, 25600, 6656, 9984):
         assert lib.oc_hadamard_order(n) == oh.pick_order(n)
     assert lib.oc_hadamard_order(1000) == 0

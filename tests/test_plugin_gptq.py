@@ -57,13 +57,13 @@ def test_legacy_layer_bits():
     cfg = G.MixedGPTQConfig.from_config({"layer_bits": [4, 4, 2], "group_size": 128})
     assert len(cfg.quantization_bits) == 3 and cfg.group_size == 128
     m = cfg.get_quant_method(_layer(), "model.layers.2.mlp.down_proj")
-    assert isinstance(m, G.GPTQLinearMethod) and m.quant_config.weight_bits == 2
+    assert isinstance(m, G.MixedGPTQLinearMethod) and m.quant_config.weight_bits == 2
 
 
 def test_dispatch_per_module_group_size():
     cfg = _cfg()
     m = cfg.get_quant_method(_layer(), "model.layers.0.self_attn.o_proj")
-    assert isinstance(m, G.GPTQLinearMethod) and m.quant_config.group_size == 128
+    assert isinstance(m, G.MixedGPTQLinearMethod) and m.quant_config.group_size == 128
     m = cfg.get_quant_method(_layer(), "model.layers.0.mlp.down_proj")
     assert m.quant_config.group_size == 32 and m.quant_config.weight_bits == 2
 
@@ -109,17 +109,17 @@ def test_rotated_down_proj_is_wrapped():
 
     cfg = G.MixedGPTQConfig.from_config({"quantization_bits": QB, "rotated": True, "fp32_had": True})
     m = cfg.get_quant_method(_layer(), "model.layers.0.mlp.down_proj")
-    assert isinstance(m, ROT.RotatedLinearMethod) and isinstance(m.base_method, G.GPTQLinearMethod)
+    assert isinstance(m, ROT.RotatedLinearMethod) and isinstance(m.base_method, G.MixedGPTQLinearMethod)
     assert m.fp32_had
-    assert isinstance(cfg.get_quant_method(_layer(), "model.layers.0.mlp.up_proj"), G.GPTQLinearMethod)
+    assert isinstance(cfg.get_quant_method(_layer(), "model.layers.0.mlp.up_proj"), G.MixedGPTQLinearMethod)
     plain = G.MixedGPTQConfig.from_config({"quantization_bits": QB})
-    assert isinstance(plain.get_quant_method(_layer(), "model.layers.0.mlp.down_proj"), G.GPTQLinearMethod)
+    assert isinstance(plain.get_quant_method(_layer(), "model.layers.0.mlp.down_proj"), G.MixedGPTQLinearMethod)
 
 
 def test_rotated_wrapper_installs_one_pre_hook():
     from onecompression_amd import rotation as ROT
 
-    base = G.GPTQLinearMethod(G.GPTQLayerConfig(4, 128, False, False, "gptq"))
+    base = G.MixedGPTQLinearMethod(G.GPTQLayerConfig(4, 128, False, False, "gptq"))
     m = ROT.RotatedLinearMethod(base, fp32_had=False)
     layer = torch.nn.Module()
     m.create_weights(layer, 256, [64], 256, 64, torch.float16)
@@ -134,7 +134,7 @@ def test_rotated_wrapper_installs_one_pre_hook():
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
 @pytest.mark.parametrize("gs", [128, -1])
 def test_create_weights_shapes(bits, gs):
-    method = G.GPTQLinearMethod(G.GPTQLayerConfig(bits, gs, False, False, "gptq"))
+    method = G.MixedGPTQLinearMethod(G.GPTQLayerConfig(bits, gs, False, False, "gptq"))
     layer = torch.nn.Module()
     method.create_weights(layer, 1024, [256, 64, 64], 1024, 384, torch.float16)
     g = 1024 // 128 if gs == 128 else 1
@@ -146,7 +146,7 @@ def test_create_weights_shapes(bits, gs):
 
 def test_fused_weight_loader_places_shards():
     bits = 4
-    method = G.GPTQLinearMethod(G.GPTQLayerConfig(bits, 128, False, False, "gptq"))
+    method = G.MixedGPTQLinearMethod(G.GPTQLayerConfig(bits, 128, False, False, "gptq"))
     layer = torch.nn.Module()
     method.create_weights(layer, 256, [64, 32, 32], 256, 128, torch.float16)
     parts = {"q": 64, "k": 32, "v": 32}
@@ -204,3 +204,86 @@ def test_fused_mixed_bits_loaders_place_shards():
     for i in range(3):
         for got, want in zip(m.shard_tensors(layer, i), loaded[i]):
             assert torch.equal(got, want)
+
+
+# ---------------------------------------------------------------- weight-loader selection
+# vLLM hands a linear layer's params the v2 weight loader when the quant method's class name is on
+# WEIGHT_LOADER_V2_SUPPORTED, else the v1 loader (vllm_plugins/utils/rotation.py:126-144).  The
+# stand-in LinearBase makes the same choice; these tests hold the plugin to it.
+
+@pytest.mark.skipif(HAS_VLLM, reason="exercises the stand-in LinearBase's loader selection")
+def test_gptq_method_gets_the_v1_loader_and_loads_fused_shards():
+    from onecompression_amd import synth
+    from onecompression_amd.vllm_compat import WEIGHT_LOADER_V2_SUPPORTED
+
+    assert "GPTQLinearMethod" in WEIGHT_LOADER_V2_SUPPORTED  # vLLM's own GPTQ method takes v2
+    assert "MixedGPTQLinearMethod" not in WEIGHT_LOADER_V2_SUPPORTED
+    qb = [{"self_attn.q_proj": {"bits": 3, "method": "gptq", "group_size": 128},
+           "self_attn.k_proj": {"bits": 3, "method": "gptq", "group_size": 128},
+           "self_attn.v_proj": {"bits": 3, "method": "gptq", "group_size": 128}}]
+    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": qb, "checkpoint_format": "gptq"})
+    sizes = [128, 64, 64]
+    layer = LinearBase(256, 256, quant_config=cfg, prefix="model.layers.0.self_attn.qkv_proj",
+                       output_partition_sizes=sizes)
+    assert layer.loader_version == 1
+    shards = [synth.gptq_case(s, 256, n, 3, 128, False, seed=i) for i, (s, n) in enumerate(zip("qkv", sizes))]
+    for sid, c in zip("qkv", shards):
+        for name in ("qweight", "qzeros", "scales"):
+            p = getattr(layer, name)
+            p.weight_loader(p, getattr(c, name), sid)
+    assert torch.equal(layer.qweight.data, torch.cat([c.qweight for c in shards], 1))
+    assert torch.equal(layer.qzeros.data, torch.cat([c.qzeros for c in shards], 1))  # packed along N
+    assert torch.equal(layer.scales.data, torch.cat([c.scales for c in shards], 1))
+
+
+@pytest.mark.skipif(HAS_VLLM, reason="exercises the stand-in LinearBase's loader selection")
+def test_a_v2_listed_name_would_break_plain_parameters():
+    """What the method's name avoids: the same create_weights under vLLM's GPTQ method name gets
+    the v2 loader, which plain Parameters cannot serve."""
+    named_like_vllm = type("GPTQLinearMethod", (G.MixedGPTQLinearMethod,), {})
+    cfg = G.GPTQLayerConfig(4, 128, False, False, "gptq")
+
+    class _Cfg:
+        def get_quant_method(self, layer, prefix):
+            return named_like_vllm(cfg)
+
+    layer = LinearBase(256, 64, quant_config=_Cfg(), prefix="model.layers.0.mlp.up_proj")
+    assert layer.loader_version == 2
+    with pytest.raises(AttributeError):
+        layer.qweight.weight_loader(layer.qweight, torch.zeros_like(layer.qweight))
+
+
+@pytest.mark.skipif(HAS_VLLM, reason="exercises the stand-in LinearBase's loader selection")
+def test_rotation_wrapper_keeps_the_base_loader_choice():
+    """rotation.py:232-261: a v1 base keeps v1 behind RotatedLinearMethod; a v2-native base
+    (unquantized down_proj of a rotated checkpoint) gets the listed RotatedLinearMethodV2 and loads
+    through its params' own v2 methods."""
+    from onecompression_amd import rotation as ROT
+
+    qb = [{"mlp.down_proj": {"bits": 4, "method": "gptq", "group_size": 128},
+           "mlp.up_proj": {"bits": 4, "method": "gptq", "group_size": 128}}]
+    cfg = G.MixedGPTQConfig.from_config({"quantization_bits": qb, "rotated": True})
+    q = LinearBase(256, 64, quant_config=cfg, prefix="model.layers.0.mlp.down_proj")
+    assert type(q.quant_method) is ROT.RotatedLinearMethod and q.loader_version == 1
+    qb0 = [{"mlp.down_proj": {"bits": 0}}]
+    cfg0 = G.MixedGPTQConfig.from_config({"quantization_bits": qb0, "rotated": True})
+    u = LinearBase(256, 64, quant_config=cfg0, prefix="model.layers.0.mlp.down_proj")
+    assert type(u.quant_method) is ROT.RotatedLinearMethodV2 and u.loader_version == 2
+    w = torch.randn(64, 256).half()
+    u.weight.weight_loader(u.weight, w)
+    assert torch.equal(u.weight.data, w)
+
+
+def test_moe_expert_entry_preference():
+    """vllm_plugin.py:220-239: the first gate_proj entry of the layer's experts, else up, else down,
+    else any expert entry; layers past the config have none."""
+    qb = [{"mlp.experts.1.down_proj": {"bits": 2}, "mlp.experts.0.up_proj": {"bits": 3},
+           "mlp.experts.3.gate_proj": {"bits": 4}, "mlp.experts.2.gate_proj": {"bits": 8}},
+          {"mlp.experts.0.down_proj": {"bits": 2}, "mlp.experts.0.w_extra": {"bits": 3}},
+          {"mlp.experts.0.w_extra": {"bits": 3}, "self_attn.q_proj": {"bits": 4}}]
+    cfg = G.MixedGPTQConfig(quantization_bits=qb)
+    assert cfg._lookup_moe_expert_config(0)["bits"] == 4
+    assert cfg._lookup_moe_expert_config(1)["bits"] == 2
+    assert cfg._lookup_moe_expert_config(2)["bits"] == 3
+    assert cfg._lookup_moe_expert_config(3) is None
+    assert cfg._resolve_group_size(None) == cfg.group_size
