@@ -67,13 +67,37 @@ def _call_name(call):
     return "qkv_proj" if call[0].name == "q_proj" else "+".join(c.name for c in call)
 
 
-def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes=1 << 30):
+def _replay_times(g, steps, replays):
+    """Per-step ms of `replays` back-to-back replays of graph g (HIP events on the replay stream)
+    and the host wall time per step of the first one (synchronised on both sides)."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    for e0, e1 in evs:
+        e0.record()
+        g.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    return [e0.elapsed_time(e1) / steps for e0, e1 in evs], wall
+
+
+def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes=1 << 30, dispatch="fused",
+                     replays=7):
+    """One decoder layer's projections per step.  dispatch "fused": the apply() calls of a
+    fused-module plugin (config 1: qkv_proj as one grouped launch, merged gate|up);
+    "reference": every projection as its own linear, the dispatch the reference can serve
+    (it rejects a qkv_proj whose shards differ in bits)."""
     import torch
 
     from onecompression_amd import ops, synth
 
     dtype = torch.float16 if dtype_name == "fp16" else torch.bfloat16
-    calls = synth.layer_calls(cfg)
+    calls = synth.layer_calls(cfg) if dispatch == "fused" else [[c] for c in synth.config_cases(cfg)]
     cases = [c for call in calls for c in call]
     flat = _prepare_copies(cases, dev, rotate_bytes)
     # per copy: the prepared parts of each call
@@ -104,17 +128,15 @@ def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes
     # graph.  The graph holds exactly `steps` steps (step i on weight copy
     # i mod copies), as a decode iteration's graph holds every layer, so no
     # graph-launch gap is charged per step.  After the eager warmup steps the
-    # graph is replayed once untimed, then once timed.
+    # graph is replayed once untimed, once timed on the host clock, then
+    # `replays` times with HIP events; the step time is the median replay.
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(steps):
             step(i)
     g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    g.replay()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
+    per_step_ms, wall_first = _replay_times(g, steps, replays)
+    wall = statistics.median(per_step_ms) * 1e-3
 
     # Per-call durations: for each apply() call, HIP events on the launch
     # stream around `steps` back-to-back launches of that call (rotating
@@ -138,7 +160,7 @@ def bench_gptq_layer(cfg, m, steps, warmup, dev, dtype_name="fp16", rotate_bytes
                         "K": call[0].in_features, "N": sum(c.out_features for c in call),
                         "bytes": b, "us": t * 1e3, "GBps": b / (t * 1e-3) / 1e9})
     return {"step_bytes": step_bytes, "wall_s": wall, "kernels": kernels, "copies": len(sets),
-            "cases": cases}
+            "cases": cases, "replay_ms_per_step": per_step_ms, "wall_first_replay_s": wall_first}
 
 
 def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 4)):
@@ -154,13 +176,15 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
     for _ in range(warmup):
         ops.gptq_gemm(x, p, out=y)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
+    # each launch between its own HIP events on the launch stream; the median launch is reported
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record()
         ops.gptq_gemm(x, p, out=y)
-    e1.record()
+        e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    times = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+    ms = statistics.median(times)
     tflops = 2.0 * m * k * n / (ms * 1e-3) / 1e12
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -168,6 +192,7 @@ def bench_gemm_large(m, steps, warmup, dev, shape=("gate_up_proj", 5120, 34816, 
         with open(tpath) as f:
             traffic = json.load(f).get("kernels", {}).get(f"k_gemm {name} {k}->{n} {bits}b M={m}")
     return {"workload": f"cfg4 {name} {k}->{n} {bits}b gs128 bf16", "M": m, "ms": round(ms, 4),
+            "launches": steps, "ms_min_max": [round(times[0], 4), round(times[-1], 4)],
             "TFLOPs": round(tflops, 1), "frac_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
@@ -234,7 +259,8 @@ def report_moe(dev, bits=4, gs=128, routings=16):
 
 
 def _time_graph(launch, copies, iters, warm=2):
-    """Mean µs per launch of `iters` launches (launch(i) uses copy i % copies) in one HIP graph."""
+    """µs per launch: `iters` launches (launch(i) uses copy i % copies) in one HIP graph, the median of
+    three timed replays."""
     import torch
 
     for i in range(warm):
@@ -246,12 +272,13 @@ def _time_graph(launch, copies, iters, warm=2):
             launch(i)
     g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    g.replay()
-    e1.record()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(3)]
+    for e0, e1 in evs:
+        e0.record()
+        g.replay()
+        e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / iters
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / iters
 
 
 def _entry(cfg, name, k, n, m, bits, nbytes, flops, us, dtype):
@@ -345,14 +372,30 @@ def report_configs(dev, only=None):
 
 
 def _cpu_model():
+    """The host CPU as lscpu names it (model name, family/model/stepping, sockets x cores x threads)."""
+    import subprocess
+
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        out = ""
+    f = {}
+    for line in out.splitlines():
+        if ":" in line:
+            k, v = line.split(":", 1)
+            f[k.strip()] = v.strip()
+    if "Model name" not in f:
+        try:
+            with open("/proc/cpuinfo") as fh:
+                for line in fh:
+                    if line.startswith("model name"):
+                        return line.split(":", 1)[1].strip()
+        except OSError:
+            pass
+        return "unknown"
+    return (f"{f['Model name']} (family {f.get('CPU family', '?')} model {f.get('Model', '?')} stepping "
+            f"{f.get('Stepping', '?')}; {f.get('Socket(s)', '?')} socket(s) x {f.get('Core(s) per socket', '?')} "
+            f"cores x {f.get('Thread(s) per core', '?')} threads)")
 
 
 def cpu_baseline(cases, m, budget_s=20.0, min_runs=3, max_runs=10, warmup=1):
@@ -496,6 +539,21 @@ def main():
         print(json.dumps({"moe": report_moe(dev)}))
         return
     r = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev)
+    ref_dispatch = None
+    if args.config == 1:
+        # the same layer with every projection as its own linear (what the reference can serve: it
+        # rejects a qkv_proj whose shards differ in bits); weights of the fused run freed first
+        torch.cuda.empty_cache()
+        rr = bench_gptq_layer(args.config, args.m, args.steps, args.warmup, dev, dispatch="reference")
+        ref_dispatch = {"value": round(rr["step_bytes"] / rr["wall_s"] / 1e9, 1), "unit": "GB/s",
+                        "ms_per_step": round(rr["wall_s"] * 1e3, 4),
+                        "frac_hbm_peak": round(rr["step_bytes"] / rr["wall_s"] / 1e9 / HBM_PEAK_GBS, 4),
+                        "calls": "q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj (7 launches)",
+                        "replay_ms_per_step": [round(v, 5) for v in rr["replay_ms_per_step"]],
+                        "per_kernel": [{k: (round(v, 2) if isinstance(v, float) else v) for k, v in kk.items()}
+                                       for kk in rr["kernels"]]}
+        del rr
+        torch.cuda.empty_cache()
     dom = max(r["kernels"], key=lambda k: k["us"])
     value = r["step_bytes"] / r["wall_s"] / 1e9
     # the wide dominant layer's kernel at M <= 4 (k_gemv_stream_bal at M >= 3 when its n-tiles load
@@ -518,6 +576,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["wall_s"] * 1e3, 4),
+        "timing": {"method": f"median of {len(r['replay_ms_per_step'])} replays (HIP events) of a graph "
+                             f"of {args.steps} steps",
+                   "replay_ms_per_step": [round(v, 5) for v in r["replay_ms_per_step"]],
+                   "first_replay_host_clock_ms_per_step": round(r["wall_first_replay_s"] * 1e3, 5)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -536,9 +598,11 @@ def main():
         "per_kernel": [{k: (round(v, 2) if isinstance(v, float) else v) for k, v in kk.items()}
                        for kk in r["kernels"]],
     }
+    if ref_dispatch is not None:
+        out["reference_dispatch"] = ref_dispatch
     if not args.no_secondary:
         try:
-            out["secondary"] = bench_gemm_large(2048, 5, 2, dev)
+            out["secondary"] = bench_gemm_large(2048, 21, 3, dev)
         except Exception as e:  # the large-M measurement is reported, never hides the main line
             out["secondary"] = {"error": str(e)}
     if not args.no_configs:
@@ -552,7 +616,7 @@ def main():
         except Exception as e:  # reported, never hides the main line
             out["moe"] = {"error": str(e)}
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(r["cases"], args.m)
+        out["cpu_baseline"] = cpu_baseline(r["cases"], args.m, budget_s=0.0, min_runs=10, max_runs=10, warmup=2)
         c0 = synth_config0()
         out["cpu_baseline_cfg0"] = {f"M={mm}": cpu_baseline(c0, mm, budget_s=15.0, min_runs=10, max_runs=10,
                                                              warmup=2) for mm in (1, 16)}
