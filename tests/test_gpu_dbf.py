@@ -61,8 +61,6 @@ def test_sign_matmul_known_answer(dev):
                                    (512, 384, 130), (640, 1000, 300), (4096, 14336, 160)])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_dbf_forward(dev, k, n, m, dtype):
-    if dtype == "bf16" and k * n > 4096 * 4096:
-        pytest.skip("bf16 covered at small shapes")
     r, bp1, bp3, s0, s2, s4 = _factors(k, n, k + n + m)
     td = torch.float16 if dtype == "fp16" else torch.bfloat16
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(td)
@@ -174,3 +172,40 @@ def test_sign_gemm_fill_and_bias(dev, dtype, m):
     assert _rel(o[:, :R].numpy(), ref.numpy()) <= 1e-2
     assert torch.all(o[:, R:fill_to] == 0)
     assert torch.all(o[:, fill_to:] == 7.0)
+
+
+# 16 < M <= 64 on the large-M GEMM core (64-row tiles, K split with fp32 partials and a fixup):
+# pre and post scales, bias, fill_to of the rank stage, a rank stage of one-k-block units, bf16,
+# and the two-term MDBF stage.
+@pytest.mark.parametrize("m", [17, 32, 48, 64])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_dbf_mid_m(dev, m, dtype):
+    k, n = 1408, 720  # r = 476: rank stage 30 tiles x 11 k-blocks, output stage 45 tiles x 4 k-blocks
+    r, bp1, bp3, s0, s2, s4 = _factors(k, n, 900 + m)
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(td)
+    prep = dbf_ops.dbf_prepare(_t(s0, dev), _t(bp1, dev), _t(s2, dev), _t(bp3, dev), _t(s4, dev), k, r, n)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.05).to(td)
+    y = dbf_ops.dbf_forward(x.to(dev), [prep], bias=bias.to(dev)).float().cpu().numpy()
+    if dtype == "bf16":
+        xn = x.view(torch.int16).numpy().view(np.uint16)
+        sc = [og.f32_to_bf16_bits(v.astype(np.float32)) for v in (s0, s2, s4)]
+        bn = bias.view(torch.int16).numpy().view(np.uint16)
+    else:
+        xn, sc, bn = x.numpy(), [s0, s2, s4], bias.numpy()
+    ref = od.dbf_forward(xn, sc[0], bp1, sc[1], bp3, sc[2], k, r, n, dtype=dtype, bias=bn)
+    assert _rel(y, ref) <= (2e-3 if dtype == "fp16" else 8e-3), _rel(y, ref)
+
+
+@pytest.mark.parametrize("m", [24, 32])
+def test_mdbf_mid_m_two_paths(dev, m):
+    n, mm = 400, 272
+    r = od.mid_features(1.0, mm, n)
+    paths = [_mdbf_path(n, mm, r, 1, 700 + i) for i in range(2)]
+    preps = [dbf_ops.mdbf_prepare_path(_t(p["A_sign_packed"], dev), p["A_shape"], _t(p["B_sign_packed"], dev),
+                                       p["B_shape"], _t(p["A_amp"], dev), _t(p["B_amp"], dev),
+                                       _t(p["Q_U_amp"], dev), _t(p["Q_V_amp"], dev)) for p in paths]
+    x = torch.randn(m, mm, generator=torch.Generator().manual_seed(9)).half()
+    y = dbf_ops.mdbf_forward(x.to(dev), preps).float().cpu().numpy()
+    ref = od.mdbf_forward(x.numpy(), paths)
+    assert _rel(y, ref) <= 2e-3, _rel(y, ref)
