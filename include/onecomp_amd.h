@@ -233,8 +233,8 @@ typedef struct {
 
 /* Device workspace bytes oc_sign_gemm needs for these terms at M rows (host only).  0 while M is
  * below the large-M threshold (the GEMV path needs none); otherwise the pre-scaled inputs
- * RNE(in * pre) of the terms that have a pre scale plus fp32 partial tiles (split tail, or one
- * slot per term and tile when n_terms > 1). */
+ * RNE(in * pre) of the terms that have a pre scale plus the fp32 partial tiles of the K-split
+ * pieces (all terms are summed in one accumulation). */
 size_t oc_sign_workspace_bytes(const oc_sign_term* terms, int n_terms, int M, int R);
 
 /* out[m, n] = sum over terms of the term above (+ bias[n]) for n < R, rounded once to act_dtype;

@@ -392,44 +392,74 @@ __global__ void k_prescale(const uint16_t* __restrict__ in, int ld_in, const uin
   xs[(size_t)m * ldx + k] = v;
 }
 
+// Several terms' inputs side by side: xs[m, off[t] + k] = RNE(in_t[m, k] * pre_t[k]) (in_t[m, k]
+// without a pre scale) for k < Kd_t, 0 for Kd_t <= k < off[t + 1] - off[t].
+struct PrescaleTerms {
+  const uint16_t* in[4];
+  const uint16_t* pre[4];
+  int ld_in[4], Kd[4], off[5];
+  int n_terms, ldx;
+};
+
+template <bool BF16>
+__global__ void k_prescale_terms(const PrescaleTerms p, uint16_t* __restrict__ xs) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (c >= p.ldx) return;
+  const int t = (c >= p.off[1]) + (c >= p.off[2]) + (c >= p.off[3]);
+  const int k = c - (t == 0 ? p.off[0] : (t == 1 ? p.off[1] : (t == 2 ? p.off[2] : p.off[3])));
+  const uint16_t* in = t == 0 ? p.in[0] : (t == 1 ? p.in[1] : (t == 2 ? p.in[2] : p.in[3]));
+  const uint16_t* pre = t == 0 ? p.pre[0] : (t == 1 ? p.pre[1] : (t == 2 ? p.pre[2] : p.pre[3]));
+  const int ld = t == 0 ? p.ld_in[0] : (t == 1 ? p.ld_in[1] : (t == 2 ? p.ld_in[2] : p.ld_in[3]));
+  const int kd = t == 0 ? p.Kd[0] : (t == 1 ? p.Kd[1] : (t == 2 ? p.Kd[2] : p.Kd[3]));
+  uint16_t v = 0;
+  if (k < kd) {
+    v = in[(size_t)m * ld + k];
+    if (pre) v = BF16 ? oc_f2bf(oc_bf2f(v) * oc_bf2f(pre[k])) : oc_f2h(oc_h2f(v) * oc_h2f(pre[k]));
+  }
+  xs[(size_t)m * p.ldx + c] = v;
+}
+
 __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int c1) {
   const int c = c0 + threadIdx.x;
   if (c < c1) out[(size_t)blockIdx.x * ld_out + c] = 0;
 }
 
 struct SignGemmPlan {
-  oc_gemm::GemmPlan gp;  // tiling of one term
+  oc_gemm::GemmPlan gp;  // tiling (MDBF: over the terms' concatenated k-blocks)
   int mt;                // tile height 64 mt
-  size_t xs_off[kMaxTerms], part_off, bytes;
+  int nkb[kMaxTerms];    // k-blocks of each term
+  size_t xs_bytes, part_off, bytes;
 };
 
+// One term: its input (RNE(in * pre) staged when it has a pre scale), K-split
+// pieces and their fixup.  Several terms (MDBF) run as one GEMM over their
+// concatenated k-blocks (inputs staged side by side, each term's post scale
+// folded into its +-1 operand), so a term adds K, not another output pass.
 SignGemmPlan plan_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R) {
   SignGemmPlan p;
-  const SignLayout L = make_sign_layout(R, terms[0].Kd);
+  const SignLayout L0 = make_sign_layout(R, terms[0].Kd);
   const int e = oc::knob("OC_GEMM_MT", 0);
-  p.mt = (e == 1 || e == 2 || e == 4) ? e : oc_gemm::gemm_tile_height(M, L.RT * 16);
-  // several terms are summed through partial slots: no K split inside a term
-  p.gp = oc_gemm::plan_gemm(M, L.RT * 16, L.K_pad, n_terms > 1 ? 1 : oc::knob("OC_GEMM_SPLIT", 0), p.mt);
-  size_t off = 0;
+  p.mt = (e == 1 || e == 2 || e == 4) ? e : oc_gemm::gemm_tile_height(M, L0.RT * 16);
+  int nkb = 0;
   for (int i = 0; i < n_terms; ++i) {
-    p.xs_off[i] = off;
-    if (terms[i].pre) off += align256((size_t)M * round8(terms[i].Kd) * 2);
+    p.nkb[i] = make_sign_layout(R, terms[i].Kd).K_pad / 128;
+    nkb += p.nkb[i];
   }
-  p.part_off = off;
-  if (n_terms > 1)
-    off += (size_t)p.gp.MB * p.gp.NB * n_terms * (64 * p.mt) * oc_gemm::kGemmBN * 4;
-  else
-    off += align256(p.gp.part_bytes);
-  p.bytes = off;
+  p.gp = oc_gemm::plan_gemm(M, L0.RT * 16, nkb * 128, oc::knob("OC_GEMM_SPLIT", 0), p.mt);
+  if (n_terms > 1) p.xs_bytes = align256((size_t)M * nkb * 128 * 2);
+  else p.xs_bytes = terms[0].pre ? align256((size_t)M * round8(terms[0].Kd) * 2) : 0;
+  p.part_off = p.xs_bytes;
+  p.bytes = p.xs_bytes + align256(p.gp.part_bytes);
   return p;
 }
 
-template <bool BF16>
-void launch_sign_gemm_term(const oc_gemm::GemmArgs& g, int mt, int grid, hipStream_t st) {
-  const size_t lds = 2 * (size_t)(64 * mt) * 256;
-  if (mt == 1) hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 1>), dim3(grid), dim3(256), lds, st, g);
-  else if (mt == 2) hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 2>), dim3(grid), dim3(256), lds, st, g);
-  else hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 4>), dim3(grid), dim3(256), lds, st, g);
+template <bool BF16, bool MULTI>
+void launch_sign_gemm(const oc_gemm::GemmArgs& g, int mt, int grid, hipStream_t st) {
+  const size_t lds = oc_gemm::gemm_lds_bytes(mt);
+  if (mt == 1) hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 1, false, MULTI>), dim3(grid), dim3(256), lds, st, g);
+  else if (mt == 2) hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 2, false, MULTI>), dim3(grid), dim3(256), lds, st, g);
+  else hipLaunchKernelGGL((oc_gemm::k_gemm<1, 4, BF16, 4, false, MULTI>), dim3(grid), dim3(256), lds, st, g);
 }
 
 template <bool BF16>
@@ -446,31 +476,42 @@ int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool b
   OC_REQUIRE(ws_bytes >= p.bytes && (p.bytes == 0 || workspace), OC_ERR_WORKSPACE,
              "workspace of %zu bytes is smaller than the %zu required", ws_bytes, p.bytes);
   uint8_t* ws = (uint8_t*)workspace;
-  for (int i = 0; i < n_terms; ++i) {
-    const oc_sign_term& T = terms[i];
-    const SignLayout L = make_sign_layout(R, T.Kd);
-    oc_gemm::GemmArgs g = {};
+  const SignLayout L0 = make_sign_layout(R, terms[0].Kd);
+  // Columns R .. fill_to of the output (the next stage's zero padding) come
+  // out of the GEMM as zeros when there is no bias: their scale is 0 (finite
+  // inputs, 0 times a finite sum).
+  const bool fold_fill = fill_to > R && bias == nullptr && fill_to <= L0.RT * 16;
+  oc_gemm::GemmArgs g = {};
+  g.y = (uint16_t*)out;
+  g.part = (float*)(ws + p.part_off);
+  g.bias = (const uint16_t*)bias;
+  g.M = M;
+  g.N = fold_fill ? fill_to : R;
+  g.npost = R;
+  g.N_pad = L0.RT * 16;
+  g.NT_total = L0.RT;
+  g.NU = L0.NU;
+  g.G = 1;
+  g.gshift = -1;
+  g.uk_shift = L0.UK == 4 ? 2 : (L0.UK == 2 ? 1 : 0);
+  g.MB = p.gp.MB;
+  g.NB = p.gp.NB;
+  g.NKB = p.gp.NKB;
+  g.gs = g.NKB * 128;
+  g.ldy = ld_out;
+  g.tiles_main = p.gp.tiles_main;
+  g.S = p.gp.S;
+  g.kper = p.gp.kper;
+  g.pstride = p.gp.S;
+  g.poff = 0;
+  if (n_terms == 1) {
+    const oc_sign_term& T = terms[0];
     g.w = (const uint8_t*)T.packed;
     g.post = (const uint16_t*)T.post;
-    g.y = (uint16_t*)out;
-    g.part = (float*)(ws + p.part_off);
-    g.M = M;
     g.K = T.Kd;
-    g.N = R;
-    g.N_pad = L.RT * 16;
-    g.NT_total = L.RT;
-    g.NU = L.NU;
-    g.G = 1;
-    g.gs = L.K_pad;
-    g.gshift = -1;
-    g.NKB = L.K_pad / 128;
-    g.MB = p.gp.MB;
-    g.NB = p.gp.NB;
-    g.ldy = ld_out;
-    g.uk_shift = L.UK == 4 ? 2 : (L.UK == 2 ? 1 : 0);
     if (T.pre) {
       const int ldx = round8(T.Kd);
-      uint16_t* xs = (uint16_t*)(ws + p.xs_off[i]);
+      uint16_t* xs = (uint16_t*)ws;
       const dim3 pg((ldx + 255) / 256, M);
       if (bf16)
         hipLaunchKernelGGL(k_prescale<true>, pg, dim3(256), 0, st, (const uint16_t*)T.in, T.ld_in,
@@ -485,38 +526,54 @@ int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool b
       g.x = (const uint16_t*)T.in;
       g.ldx = T.ld_in;
     }
-    if (n_terms == 1) {
-      g.bias = (const uint16_t*)bias;
-      g.tiles_main = p.gp.tiles_main;
-      g.S = p.gp.S;
-      g.kper = p.gp.kper;
-      g.pstride = p.gp.S;
-      g.poff = 0;
-    } else {  // every tile is one partial slot of this term
-      g.bias = nullptr;
-      g.tiles_main = 0;
-      g.S = 1;
-      g.kper = g.NKB;
-      g.pstride = n_terms;
-      g.poff = i;
+  } else {
+    // the terms' inputs side by side, k-block aligned (zeros past each Kd)
+    PrescaleTerms pt = {};
+    int off = 0;
+    for (int i = 0; i < n_terms; ++i) {
+      pt.in[i] = (const uint16_t*)terms[i].in;
+      pt.pre[i] = (const uint16_t*)terms[i].pre;
+      pt.ld_in[i] = terms[i].ld_in;
+      pt.Kd[i] = terms[i].Kd;
+      pt.off[i] = off;
+      g.tkb[i] = off / 128;
+      g.tw[i] = (const uint8_t*)terms[i].packed;
+      g.tpost[i] = (const uint16_t*)terms[i].post;
+      g.tNU[i] = make_sign_layout(R, terms[i].Kd).NU;
+      off += p.nkb[i] * 128;
     }
-    const int grid = n_terms == 1 ? p.gp.tiles_main + p.gp.split_tiles * p.gp.S : p.gp.MB * p.gp.NB;
-    if (bf16) launch_sign_gemm_term<true>(g, p.mt, grid, st);
-    else launch_sign_gemm_term<false>(g, p.mt, grid, st);
+    for (int i = n_terms; i <= kMaxTerms; ++i) {
+      pt.off[i] = off;
+      g.tkb[i] = off / 128;
+    }
+    pt.n_terms = n_terms;
+    pt.ldx = off;
+    uint16_t* xs = (uint16_t*)ws;
+    const dim3 pg((off + 255) / 256, M);
+    if (bf16) hipLaunchKernelGGL(k_prescale_terms<true>, pg, dim3(256), 0, st, pt, xs);
+    else hipLaunchKernelGGL(k_prescale_terms<false>, pg, dim3(256), 0, st, pt, xs);
     OC_HIP(hipGetLastError());
-    if (i == n_terms - 1) {
-      const int fix_tiles = n_terms == 1 ? p.gp.split_tiles : p.gp.MB * p.gp.NB;
-      if (fix_tiles > 0) {
-        g.bias = (const uint16_t*)bias;
-        g.tiles_main = n_terms == 1 ? p.gp.tiles_main : 0;
-        g.pstride = n_terms == 1 ? p.gp.S : n_terms;
-        if (bf16) launch_sign_fixup<true>(g, p.mt, fix_tiles, st);
-        else launch_sign_fixup<false>(g, p.mt, fix_tiles, st);
-        OC_HIP(hipGetLastError());
-      }
-    }
+    g.x = xs;
+    g.ldx = off;
+    g.K = off;
+    g.w = g.tw[0];
+    g.nterms = n_terms;
   }
-  if (fill_to > R) {
+  const int grid = p.gp.tiles_main + p.gp.split_tiles * p.gp.S;
+  if (n_terms == 1) {
+    if (bf16) launch_sign_gemm<true, false>(g, p.mt, grid, st);
+    else launch_sign_gemm<false, false>(g, p.mt, grid, st);
+  } else {
+    if (bf16) launch_sign_gemm<true, true>(g, p.mt, grid, st);
+    else launch_sign_gemm<false, true>(g, p.mt, grid, st);
+  }
+  OC_HIP(hipGetLastError());
+  if (p.gp.split_tiles > 0) {
+    if (bf16) launch_sign_fixup<true>(g, p.mt, p.gp.split_tiles, st);
+    else launch_sign_fixup<false>(g, p.mt, p.gp.split_tiles, st);
+    OC_HIP(hipGetLastError());
+  }
+  if (fill_to > R && !fold_fill) {
     hipLaunchKernelGGL(k_zero_cols, dim3(M), dim3(64), 0, st, (uint16_t*)out, ld_out, R, fill_to);
     OC_HIP(hipGetLastError());
   }

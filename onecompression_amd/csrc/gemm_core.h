@@ -14,6 +14,8 @@
 
 namespace oc_gemm {
 
+constexpr int kGemmMaxTerms = 4;
+
 struct GemmArgs {
   const uint16_t* x;     // [M, ldx] activations (16-bit), K valid columns
   const uint8_t* w;      // packed codes (lane-chunk layout) or sign words
@@ -37,6 +39,18 @@ struct GemmArgs {
   const int* gcount;
   size_t gw_stride, gmeta_stride;
   int gbias_stride;
+  // signs: columns npost .. N - 1 have no scale and come out as zeros
+  int npost;
+  // signs, k_gemm<.., MULTI>: nterms terms summed in one accumulation (MDBF).
+  // x holds the terms' inputs side by side (k-blocks [tkb[t], tkb[t + 1]) of
+  // the concatenated K are term t's); term t reads its own sign words (tw, tNU
+  // units per row tile, 2^uk_shift k-blocks per unit for every term) and its
+  // per-column scale tpost (null: 1) is folded into its +-1 operand (post unused)
+  int nterms;
+  int tkb[kGemmMaxTerms + 1];
+  const uint8_t* tw[kGemmMaxTerms];
+  const uint16_t* tpost[kGemmMaxTerms];
+  int tNU[kGemmMaxTerms];
 };
 
 // Tile order: consecutive workgroups go to consecutive XCDs; with 8 | MB the
@@ -95,12 +109,20 @@ constexpr size_t kGemmXBuf = (size_t)kGemmBM * 256;  // bytes of one x buffer (1
 
 // Tile height 64 MT rows (MT = 1, 2, 4; 256 columns always): each wave holds
 // NI = 2 MT m32-tiles of its 64 columns and loads XJ = 4 MT KB of each x block.
+// (Prefetching x three k-blocks ahead instead of one, into four buffers, was
+// measured at 64- and 128-row tiles and M <= 512: no change.)
 template <int MT>
 struct GemmTile {
   static_assert(MT == 1 || MT == 2 || MT == 4, "tile height 64, 128 or 256");
   static constexpr int BM = 64 * MT, NI = 2 * MT, XJ = 4 * MT;
   static constexpr size_t XBUF = (size_t)BM * 256;  // bytes of one x buffer
+  static constexpr size_t LDS = 2 * XBUF;           // two buffers alternate per k-block
 };
+
+// Dynamic LDS bytes of a k_gemm launch with tile height 64 mt.
+inline size_t gemm_lds_bytes(int mt) {
+  return mt == 1 ? GemmTile<1>::LDS : (mt == 2 ? GemmTile<2>::LDS : GemmTile<4>::LDS);
+}
 
 typedef __attribute__((address_space(3))) void* oc_lds_ptr;
 
@@ -173,7 +195,18 @@ struct GemmLoads {
   static constexpr int n = 4 * per + (BITS == 1 ? 0 : 2 * (4 / CS));
 };
 
-template <int BITS, int CS, bool BF16, int MT = 4, bool GROUPED = false>
+// Term of concatenated k-block kb (uniform; compares, no dynamic indexing of
+// the kernel arguments; tkb[t] of absent terms is past every k-block).
+__device__ __forceinline__ int gemm_term(const GemmArgs& a, int kb) {
+  return (kb >= a.tkb[1]) + (kb >= a.tkb[2]) + (kb >= a.tkb[3]);
+}
+
+template <typename T>
+__device__ __forceinline__ T gemm_pick(int t, T v0, T v1, T v2, T v3) {
+  return t == 0 ? v0 : (t == 1 ? v1 : (t == 2 ? v2 : v3));
+}
+
+template <int BITS, int CS, bool BF16, int MT = 4, bool GROUPED = false, bool MULTI = false>
 __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   using TL = GemmTile<MT>;
   constexpr int NI = TL::NI;
@@ -247,19 +280,26 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   // ahead into one of three rotating register sets.  Each set costs exactly
   // GemmLoads<BITS, CS>::n vector-memory instructions (no two of its loads are
   // adjacent in memory, so none are merged), which the vmcnt waits rely on.
-  uint32_t w0[2][2][NWB], w1[2][2][NWB], w2[2][2][NWB];
-  uint32_t m0w[2][SPK], m1w[2][SPK], m2w[2][SPK];
   auto load_w = [&](int kb, uint32_t (&wb)[2][2][NWB], uint32_t (&mw)[2][SPK]) {
     using GG = Geo<SIGN ? 4 : BITS>;
     const int u = kb / GG::U, kbl = kb % GG::U;
 #pragma unroll
     for (int T = 0; T < 2; ++T) {
       if constexpr (SIGN) {
-        // word (rt, unit, lane, kbl) of the sign layout
-        const int su = kb >> a.uk_shift, skb = kb & ((1 << a.uk_shift) - 1);
+        // word (rt, unit, lane, kbl) of the sign layout (MULTI: of the k-block's term)
+        const uint8_t* ws = wsrc;
+        int nu = a.NU, kbl = kb;
+        if constexpr (MULTI) {
+          const int t = gemm_term(a, kb);
+          kbl = kb - gemm_pick(t, a.tkb[0], a.tkb[1], a.tkb[2], a.tkb[3]);
+          ws = gemm_pick(t, a.tw[0], a.tw[1], a.tw[2], a.tw[3]);
+          nu = gemm_pick(t, a.tNU[0], a.tNU[1], a.tNU[2], a.tNU[3]);
+          mw[T][0] = (uint32_t)t;  // selects the term's operand scale (no load)
+        }
+        const int su = kbl >> a.uk_shift, skb = kbl & ((1 << a.uk_shift) - 1);
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2)
-          wb[T][q2][0] = *((const uint32_t*)wsrc + ((((size_t)nt[T] * a.NU + su) * 64 + cl[q2]) << a.uk_shift) + skb);
+          wb[T][q2][0] = *((const uint32_t*)ws + ((((size_t)nt[T] * nu + su) * 64 + cl[q2]) << a.uk_shift) + skb);
       } else {
 #pragma unroll
       for (int q2 = 0; q2 < 2; ++q2) {
@@ -309,6 +349,22 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][T][r] = 0.f;
 
+  // MULTI: operand scale per term and n32-tile of this lane's column
+  // (magnitude pair and the mask that flips the signs where it is negative):
+  // post[n] (+1 without a post vector) below npost, 0 above.
+  uint32_t smag[kGemmMaxTerms][2], sneg[kGemmMaxTerms][2];
+  if constexpr (SIGN && MULTI) {
+#pragma unroll
+    for (int t = 0; t < kGemmMaxTerms; ++t)
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const int n = n0 + 32 * T + (lane & 31);
+        const uint16_t* pp = gemm_pick(t, a.tpost[0], a.tpost[1], a.tpost[2], a.tpost[3]);
+        const uint32_t p = (t < a.nterms && n < a.npost) ? (pp ? (uint32_t)pp[n] : (mag & 0xFFFFu)) : 0u;
+        smag[t][T] = (p & 0x7FFFu) * 0x00010001u;
+        sneg[t][T] = (p & 0x8000u) ? 0xFFFFFFFFu : 0u;
+      }
+  }
   // B operands of step s (both n32-tiles); dq holds the scale terms of the
   // current group and is refreshed when a new group starts.
   auto make_b = [&](const uint32_t (&wb)[2][2][NWB], const uint32_t (&mw)[2][SPK], int s, oc_u4 (&B)[2],
@@ -317,10 +373,21 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     for (int T = 0; T < 2; ++T) {
       if constexpr (SIGN) {
         // pairs 4t .. 4t+3 of the lane's word: bits 15-P / 31-P, set for -1
-        const uint32_t w = wb[T][s & 1][0];
         const int P = 4 * (s >> 1);
-        B[T] = oc_u4{((w << P) & msk) | mag, ((w << (P + 1)) & msk) | mag, ((w << (P + 2)) & msk) | mag,
-                     ((w << (P + 3)) & msk) | mag};
+        if constexpr (MULTI) {  // the term's scale: dq = (magnitude pair, sign-flip mask)
+          if (s == 0) {
+            const int t = (int)mw[T][0];
+            dq[T].a = gemm_pick(t, smag[0][T], smag[1][T], smag[2][T], smag[3][T]);
+            dq[T].b = gemm_pick(t, sneg[0][T], sneg[1][T], sneg[2][T], sneg[3][T]);
+          }
+          const uint32_t w = wb[T][s & 1][0] ^ dq[T].b, pm = dq[T].a;
+          B[T] = oc_u4{((w << P) & msk) | pm, ((w << (P + 1)) & msk) | pm, ((w << (P + 2)) & msk) | pm,
+                       ((w << (P + 3)) & msk) | pm};
+        } else {
+          const uint32_t w = wb[T][s & 1][0];
+          B[T] = oc_u4{((w << P) & msk) | mag, ((w << (P + 1)) & msk) | mag, ((w << (P + 2)) & msk) | mag,
+                       ((w << (P + 3)) & msk) | mag};
+        }
       } else {
         if (s == 0 || (CS == 1 && (s & 1) == 0)) dq[T] = gemm_deq<BF16>(mw[T][(s >> 1) / CS]);
         B[T] = gemm_apply<BF16>(decode_step<BITS, false>(wb[T][s & 1], s >> 1, msk, mag), dq[T]);
@@ -388,6 +455,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
     asm volatile("s_barrier" ::: "memory");
   };
 
+  uint32_t w0[2][2][NWB], w1[2][2][NWB], w2[2][2][NWB];
+  uint32_t m0w[2][SPK], m1w[2][SPK], m2w[2][SPK];
   load_x(kb0, 0);
   load_w(kb0, w0, m0w);
   load_w(min(kb0 + 1, last), w1, m1w);
@@ -405,12 +474,13 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   // the last body prefetched into the idle x buffer: let it land before exit
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  float ps[2] = {1.f, 1.f};  // per-column post scale (signs)
-  if (a.post) {
+  float ps[2] = {1.f, 1.f};  // per-column post scale (single-operand signs; 0 past npost)
+  if constexpr (SIGN && !MULTI) {
 #pragma unroll
     for (int T = 0; T < 2; ++T) {
       const int n = n0 + 32 * T + (lane & 31);
-      if (n < a.N) ps[T] = BF16 ? oc_bf2f(a.post[n]) : oc_h2f(a.post[n]);
+      if (n >= a.npost) ps[T] = 0.f;
+      else if (a.post) ps[T] = BF16 ? oc_bf2f(a.post[n]) : oc_h2f(a.post[n]);
     }
   }
   if (piece) {
@@ -422,7 +492,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
 #pragma unroll
       for (int T = 0; T < 2; ++T)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pp[((i * 2 + T) * 16 + r) * 64] = acc[i][T][r] * ps[T];
+        for (int r = 0; r < 16; ++r)  // rows past M are never read by the fixup (skipped below 256-row tiles)
+          if (MT == 4 || m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3) < mlim)
+            pp[((i * 2 + T) * 16 + r) * 64] = acc[i][T][r] * ps[T];
     return;
   }
   // epilogue: register r of tile (i, T) is row 32i + 8(r/4) + 4h + r%4, column n0 + 32T + lane%32

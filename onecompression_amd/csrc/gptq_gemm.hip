@@ -763,6 +763,10 @@ struct StreamArgs {
   uint16_t* y;
   int M, K, K_pad, N, N_pad, NT_total, NU, G, gs, gkb_shift, ldy;
   int tpw;  // k_gemv_stream_bal: n-tiles per workgroup
+  // k_gemm_stream: split blockIdx.y takes units [y NU / S, (y + 1) NU / S) and, with S > 1,
+  // writes fp32 partial[((y M + m) N_pad + n)] for k_splitk_reduce
+  int S;
+  float* partial;
 };
 
 template <int BITS, int D, int MR, int KS, bool BF16>
@@ -1066,13 +1070,20 @@ __global__ __launch_bounds__(64 * kStreamBalWaves) void k_gemv_stream_bal(const 
 }
 
 // ---------------------------------------------------------------------------
-// Wide layers at mid M (up to 64 rows): the same one-wave-per-n-tile stream
-// over K, with x staged one k-block (128 k) at a time in a two-buffer LDS
-// ring shared by the workgroup's 4 waves, one barrier per k-block.  Each
-// decoded B operand feeds MB = ceil(M / 16) MFMAs (the 16-row blocks of x).
-// The staging loads of k-block kb + 2 are issued while kb is computed; the
-// rows' sums over each k-block (for the zero-point correction) are formed
-// from the staged registers with a 16-lane butterfly, once per workgroup.
+// Mid M (up to 128 rows): one wave per n-tile streams its split of K, with x
+// staged one k-block (128 k) at a time in a two-buffer LDS ring shared by the
+// workgroup's 4 waves, one barrier per k-block.  Each decoded B operand feeds
+// MB = ceil(M / 16) MFMAs (the 16-row blocks of x).  The staging loads of
+// k-block kb + 2 are issued while kb is computed.
+// MB <= 2: codes decode to (off + q) and the zero point and scale are applied
+// to the sums, y += s (sum x (off + q) - (off + z) sum x), with the rows' sums
+// over each k-block formed from the staged registers (16-lane butterfly).
+// MB >= 4: that correction would cost more than the weights it saves, so the
+// B operand is the dequantised weight RNE(s (q - z)) itself (the large-M
+// GEMM's arithmetic, bit for bit) and no sums are formed.
+// The k-block barrier waits for LDS traffic only: __syncthreads() also waits
+// for every outstanding global load, i.e. for the x and weight prefetches,
+// which would expose a memory round trip per k-block.
 // ---------------------------------------------------------------------------
 template <int BITS, int MB, bool BF16>
 __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
@@ -1081,17 +1092,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
   constexpr int D = 2;        // units in flight per wave
   constexpr int XLD = 136;    // halfs per staged row (128 + 8 pad)
   constexpr int ROWS = 16 * MB;
+  constexpr bool SUMS = MB <= 2;  // zero-point correction on the sums (else dequantised B)
   constexpr float OFF = dec_offset<BITS, BF16>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kq = lane >> 4;
-  const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<BF16>());
+  const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<SUMS && BF16>());
   const int nt = blockIdx.x * 4 + wave;
   const int ntc = min(nt, a.NT_total - 1);  // waves past the last n-tile compute it, unused
   const int M = a.M;
+  // this split's units (a multiple of D: the planner keeps NU / S even)
+  const int split = blockIdx.y;
+  const int nu = a.NU / a.S, ub = split * nu;
 
   extern __shared__ __align__(16) uint16_t xl[];   // [2][ROWS][XLD]
-  float* xsum = (float*)(xl + 2 * ROWS * XLD);     // [2][ROWS]
+  float* xsum = (float*)(xl + 2 * ROWS * XLD);     // [2][ROWS] (SUMS only)
 
   // staging of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at 8 (c % 16))
   const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.x, (uint32_t)M * a.K * 2);
@@ -1108,20 +1123,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
     for (int j = 0; j < MB; ++j) {
       const int c = threadIdx.x + 256 * j, row = c >> 4;
       *(oc_u4*)(xl + (buf * ROWS + row) * XLD + 8 * (c & 15)) = xs_reg[j];
-      float sum = 0.f;
+      if constexpr (SUMS) {
+        float sum = 0.f;
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const uint32_t pr = xs_reg[j][h];
-        sum += (BF16 ? oc_bf2f((uint16_t)(pr & 0xFFFFu)) : oc_h2f((uint16_t)(pr & 0xFFFFu))) +
-               (BF16 ? oc_bf2f((uint16_t)(pr >> 16)) : oc_h2f((uint16_t)(pr >> 16)));
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t pr = xs_reg[j][h];
+          sum += (BF16 ? oc_bf2f((uint16_t)(pr & 0xFFFFu)) : oc_h2f((uint16_t)(pr & 0xFFFFu))) +
+                 (BF16 ? oc_bf2f((uint16_t)(pr >> 16)) : oc_h2f((uint16_t)(pr >> 16)));
+        }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+        if ((c & 15) == 0) xsum[buf * ROWS + row] = sum;
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
-      if ((c & 15) == 0) xsum[buf * ROWS + row] = sum;
     }
   };
 
-  const bool has_bias = a.bias != nullptr;
+  const bool has_bias = a.bias != nullptr && a.S == 1;
   const uint16_t braw = __builtin_amdgcn_raw_buffer_load_b16(
       oc_rsrc(a.bias, (uint32_t)a.N * 2), has_bias && nt * 16 + col < a.N ? (uint32_t)(nt * 16 + col) * 2 : kOcOob,
       0, 0);
@@ -1148,56 +1165,79 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
   oc_f4 yacc[MB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) yacc[i] = oc_f4{0.f, 0.f, 0.f, 0.f};
-  const int nkb = a.NU * U;
-  // k-block kb: x from buffer kb & 1; afterwards the staged registers of
-  // kb + 1 go to the other buffer, kb + 2 is loaded, one barrier.
+  const int kb_end = (ub + nu) * U;  // one past this split's last k-block
+  // k-block kb: x from buffer (kb - first) & 1; afterwards the staged
+  // registers of kb + 1 go to the other buffer, kb + 2 is loaded, one barrier.
   auto consume = [&](int u, const uint32_t (&w)[4 * P], const uint32_t (&m)[U]) {
 #pragma unroll
     for (int kbl = 0; kbl < U; ++kbl) {
-      const int kb = u * U + kbl, buf = kb & 1;
+      const int kb = u * U + kbl, buf = (kb - ub * U) & 1;
       oc_u4 bq[4];
-      decode_kblock<BITS, BF16>(w, kbl, bq, msk, mag);
+      decode_kblock<BITS, SUMS && BF16>(w, kbl, bq, msk, mag);
       const uint32_t md = m[kbl];
-      const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
-      const float oz = OFF + (float)(md >> 16);
+      if constexpr (SUMS) {
+        const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
+        const float oz = OFF + (float)(md >> 16);
 #pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const uint16_t* arow = xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq;
-        oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MB; ++i) {
+          const uint16_t* arow = xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq;
+          oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(*(const oc_u4*)(arow + 32 * t), bq[t], acc);
-        const oc_f4 xsv = *(const oc_f4*)(xsum + buf * ROWS + 16 * i + 4 * kq);
+          for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(*(const oc_u4*)(arow + 32 * t), bq[t], acc);
+          const oc_f4 xsv = *(const oc_f4*)(xsum + buf * ROWS + 16 * i + 4 * kq);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) yacc[i][r] = fmaf(sc, fmaf(-oz, xsv[r], acc[r]), yacc[i][r]);
+          for (int r = 0; r < 4; ++r) yacc[i][r] = fmaf(sc, fmaf(-oz, xsv[r], acc[r]), yacc[i][r]);
+        }
+      } else {
+        const oc_gemm::GemmDeq<BF16> dq = oc_gemm::gemm_deq<BF16>(md);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bq[t] = oc_gemm::gemm_apply<BF16>(bq[t], dq);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const uint16_t* arow = xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) yacc[i] = oc_mfma16<BF16>(*(const oc_u4*)(arow + 32 * t), bq[t], yacc[i]);
+        }
       }
-      stage_store(buf ^ 1);               // k-block kb + 1 (its buffer was last read at kb - 1)
-      stage_load(min(kb + 2, nkb - 1));   // past the end: reload the last k-block, unused
-      __syncthreads();
-      __builtin_amdgcn_sched_barrier(0);  // one k-block's decode at a time (register pressure)
+      stage_store(buf ^ 1);                  // k-block kb + 1 (its buffer was last read at kb - 1)
+      stage_load(min(kb + 2, kb_end - 1));   // past the end: reload the last k-block, unused
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);     // one k-block's decode at a time (register pressure)
     }
   };
-  // prologue: x of k-blocks 0 (to LDS) and 1 (in registers), D weight units
-  stage_load(0);
+  // prologue: x of this split's k-blocks 0 (to LDS) and 1 (in registers), D weight units
+  stage_load(ub * U);
   stage_store(0);
-  stage_load(min(1, nkb - 1));
+  stage_load(min(ub * U + 1, kb_end - 1));
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    load(d, wb[d], mb[d]);
+    load(ub + d, wb[d], mb[d]);
     __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();
-  for (int i0 = 0; i0 < a.NU - D; i0 += D) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  for (int i0 = 0; i0 < nu - D; i0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      consume(i0 + d, wb[d], mb[d]);
-      load(i0 + D + d, wb[d], mb[d]);
+      consume(ub + i0 + d, wb[d], mb[d]);
+      load(ub + i0 + D + d, wb[d], mb[d]);
     }
   }
 #pragma unroll
-  for (int d = 0; d < D; ++d) consume(a.NU - D + d, wb[d], mb[d]);
+  for (int d = 0; d < D; ++d) consume(ub + nu - D + d, wb[d], mb[d]);
 
   const int n = nt * 16 + col;
   if (nt < a.NT_total && n < a.N) {
+    if (a.S > 1) {
+      float* pp = a.partial + (size_t)split * M * a.N_pad + n;
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * i + 4 * kq + r;
+          if (m < M) pp[(size_t)m * a.N_pad] = yacc[i][r];
+        }
+      return;
+    }
     const float b = has_bias ? (BF16 ? oc_bf2f(braw) : oc_h2f(braw)) : 0.f;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -1288,6 +1328,7 @@ struct GemvPlan {
 };
 
 constexpr int kGemvMaxM = 16;
+constexpr int kStreamMaxM = 128;  // rows of k_gemm_stream (8 MFMA row blocks)
 constexpr size_t kGemvLds = 96 * 1024;
 
 int log2_exact(int v) {
@@ -1402,30 +1443,59 @@ size_t stream_lds(const oc::Layout& L, int M) {
   return (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 16 * 4;
 }
 
-// k_gemm_stream serves wide layers (at least 1024 n-tiles) at 12 < M <= 32
-// (and M <= 12 when x does not fit k_gemv_stream's LDS) with groups that are
-// powers of two >= 128 and an even number of units.  OC_GEMM_STREAM=0 turns
-// it off, =1 forces it where it applies.
+// k_gemm_stream serves groups that are powers of two >= 128 with an even
+// number of units: wide layers (at least 1024 n-tiles) at 12 < M <= 32 (and
+// M <= 12 when x does not fit k_gemv_stream's LDS), long-K layers (>= 64
+// k-blocks) at 16 < M <= 32, every layer at 32 < M <= 64, and short-K layers
+// (<= 32 k-blocks) at 64 < M <= 128; the tiled GEMM (or the skinny kernel)
+// takes the rest (measured per configuration-1/2 shape and M).  OC_GEMM_STREAM=0
+// turns it off, =1 forces it where it applies (up to M = 128).
 bool use_gemm_stream(const oc::Layout& L, int M, int gs) {
   const int e = oc::knob("OC_GEMM_STREAM", -1);
-  if (e == 0 || M > 32 || gs < 128 || log2_exact(gs) < 0 || (L.NU % 2) != 0) return false;
+  if (e == 0 || M > kStreamMaxM || gs < 128 || log2_exact(gs) < 0 || (L.NU % 2) != 0) return false;
   if (e == 1) return true;
+  const int nkb = L.K_pad / 128;
+  if (M > 64) return nkb <= 32;
+  if (M > 32) return true;
+  if (M > 16 && nkb >= 64) return true;
   // measured: k_gemv is faster for 4 < M <= 12, the streaming GEMM from 13 rows
   return L.NT >= 1024 && (M > 12 || (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 64 > 80 * 1024);
 }
 
+// K splits of k_gemm_stream (workgroups of 4 n-tiles): enough workgroups for
+// one per CU (two per CU on layers of >= 64 k-blocks), at most 8 splits, at
+// least 4 k-blocks per split, and an even number of units per split.
+// OC_GEMM_STREAM_S forces the count.
+int gemm_stream_split(const oc::Layout& L) {
+  const int e = oc::knob("OC_GEMM_STREAM_S", 0);
+  const int wgs = (L.NT + 3) / 4, nkb = L.K_pad / 128;
+  const int target = oc_device_cus() * (nkb >= 64 ? 2 : 1);
+  int S = e > 0 ? e : (target + wgs - 1) / wgs;
+  if (e <= 0) {
+    if (S > 8) S = 8;
+    if (S > nkb / 4) S = nkb / 4;
+  }
+  if (S > L.NU / 2) S = L.NU / 2;
+  while (S > 1 && (L.NU % (2 * S)) != 0) --S;
+  return S < 1 ? 1 : S;
+}
+
+int gemm_stream_rows(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 64 ? 4 : 8)); }
+
 template <bool BF16>
 int dispatch_gemm_stream(int bits, int M, const oc::Layout& L, const StreamArgs& a, hipStream_t st) {
-  const int mbt = M <= 16 ? 1 : 2;
-  const dim3 grid((L.NT + 3) / 4), block(256);
-  const size_t lds = (size_t)2 * 16 * mbt * 136 * 2 + (size_t)2 * 16 * mbt * 4;
+  const int mbt = gemm_stream_rows(M);
+  const dim3 grid((L.NT + 3) / 4, a.S), block(256);
+  const size_t lds = (size_t)2 * 16 * mbt * 136 * 2 + (mbt <= 2 ? (size_t)2 * 16 * mbt * 4 : 0);
 #define OC_GS(B_, MB_)                                                                      \
   if (bits == B_ && mbt == MB_) {                                                           \
     hipLaunchKernelGGL((k_gemm_stream<B_, MB_, BF16>), grid, block, lds, st, a);            \
     OC_HIP(hipGetLastError());                                                              \
     return 0;                                                                               \
   }
-  OC_GS(2, 1) OC_GS(2, 2) OC_GS(3, 1) OC_GS(3, 2) OC_GS(4, 1) OC_GS(4, 2) OC_GS(8, 1) OC_GS(8, 2)
+#define OC_GSB(B_) OC_GS(B_, 1) OC_GS(B_, 2) OC_GS(B_, 4) OC_GS(B_, 8)
+  OC_GSB(2) OC_GSB(3) OC_GSB(4) OC_GSB(8)
+#undef OC_GSB
 #undef OC_GS
   return oc::set_error(OC_ERR_UNSUPPORTED, "no streaming gemm for bits=%d M=%d", bits, M);
 }
@@ -1539,7 +1609,11 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
   size_t ws = 0;
   if (has_perm) ws += align256((size_t)M * K * 2);
   const int gs = oc::eff_group(group_size, K);
-  if ((M <= kGemvMaxM && stream_depth(L, M, gs) > 0) || use_gemm_stream(L, M, gs)) return ws;
+  if (M <= kGemvMaxM && stream_depth(L, M, gs) > 0) return ws;
+  if (use_gemm_stream(L, M, gs)) {
+    const int S = gemm_stream_split(L);
+    return S > 1 ? ws + align256((size_t)S * M * L.N_pad * 4) : ws;
+  }
   if (M <= kGemvMaxM) {
     const GemvPlan p = plan_gemv(L, M, oc::eff_group(group_size, K));
     if (p.S > 1) ws += align256((size_t)p.S * M * L.N_pad * 4);
@@ -1565,7 +1639,8 @@ extern "C" int oc_gptq_describe_plan(int M, int K, int N, int bits, int group_si
   const char* g = has_perm ? "k_gather + " : "";
   const int sd = M <= kGemvMaxM ? stream_depth(L, M, gs) : 0;
   if (sd == 0 && use_gemm_stream(L, M, gs)) {
-    snprintf(buf, len, "%sk_gemm_stream mb=%d", g, M <= 16 ? 1 : 2);
+    const int S = gemm_stream_split(L);
+    snprintf(buf, len, "%sk_gemm_stream mb=%d S=%d%s", g, gemm_stream_rows(M), S, S > 1 ? " + k_splitk_reduce" : "");
   } else if (M <= kGemvMaxM && sd > 0) {
     const int t = stream_bal_tiles(L, bits, M, stream_ksplit(L));
     if (t > 0) snprintf(buf, len, "%sk_gemv_stream_bal d=%d tiles_per_wg=%d", g, sd, t);
@@ -1634,7 +1709,11 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     a.gs = gs;
     a.gkb_shift = log2_exact(gs) - 7;
     a.ldy = ldy;
-    return bf16 ? dispatch_gemm_stream<true>(bits, M, L, a, st) : dispatch_gemm_stream<false>(bits, M, L, a, st);
+    a.S = gemm_stream_split(L);
+    a.partial = (float*)ws;
+    const int rc = bf16 ? dispatch_gemm_stream<true>(bits, M, L, a, st) : dispatch_gemm_stream<false>(bits, M, L, a, st);
+    if (rc || a.S == 1) return rc;
+    return launch_reduce(bf16, a.partial, a.S, M, N, L.N_pad, bias, y, ldy, st);
   }
   if (M <= kGemvMaxM) {
     if (sd > 0) {
@@ -1716,7 +1795,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     g.kper = gp.kper;
     g.part = (float*)ws;
     const dim3 grid(gp.tiles_main + gp.split_tiles * gp.S);
-    const size_t lds = 2 * (size_t)(64 * mt) * 256;
+    const size_t lds = oc_gemm::gemm_lds_bytes(mt);
     switch (bits) {
 #define OC_GM(B_)                                                                                   \
   case B_:                                                                                          \
@@ -2141,7 +2220,7 @@ int launch_moe(const MoeArgs& g, int bits, int cs, int w, int rm, size_t lds, in
 
 template <bool BF16>
 int launch_grouped_gemm(const GemmArgs& g, int bits, bool cs4, int mt, int grid, hipStream_t st) {
-  const size_t lds = 2 * (size_t)(64 * mt) * 256;
+  const size_t lds = oc_gemm::gemm_lds_bytes(mt);
 #define OC_GG2(B_)                                                                                           \
   if (bits == B_) {                                                                                          \
     if (!cs4) hipLaunchKernelGGL((k_gemm<B_, 1, BF16, 4, true>), dim3(grid), dim3(256), lds, st, g);        \

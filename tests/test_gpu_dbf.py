@@ -209,3 +209,47 @@ def test_mdbf_mid_m_two_paths(dev, m):
     y = dbf_ops.mdbf_forward(x.to(dev), preps).float().cpu().numpy()
     ref = od.mdbf_forward(x.numpy(), paths)
     assert _rel(y, ref) <= 2e-3, _rel(y, ref)
+
+
+# The large-M sign GEMM sums several terms in one accumulation, each term's per-column post scale
+# folded into its +-1 operand (sign flips where the scale is negative, +1 without a post vector),
+# with K-split pieces over the concatenated k-blocks; without a bias the zero columns R..fill_to
+# come out of the GEMM itself.
+@pytest.mark.parametrize("m", [40, 140])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("n_terms,with_bias", [(1, False), (3, False), (4, True)])
+def test_sign_gemm_terms_signed_scales(dev, m, dtype, n_terms, with_bias):
+    R, fill_to, ld_out = 530, 536, 544
+    kds = [300, 260, 330, 270][:n_terms]
+    td = torch.float16 if dtype == "fp16" else torch.bfloat16
+    rng = np.random.default_rng(40 + n_terms + m)
+    terms, ref = [], torch.zeros(m, R)
+    for i, kd in enumerate(kds):
+        signs = rng.choice([-1, 1], size=(R, kd))
+        f = dbf_ops.sign_prepare(_t(od.pack_binary(signs), dev), R, kd)
+        ldx = (kd + 7) // 8 * 8
+        x = torch.zeros((m, ldx), dtype=td)
+        x[:, :kd] = torch.randn(m, kd, generator=torch.Generator().manual_seed(10 + i)).to(td)
+        pre = None
+        if n_terms == 3:  # the terms of one call all have a pre scale or none
+            pre = torch.zeros(ldx, dtype=td)
+            pre[:kd] = (torch.rand(kd, generator=torch.Generator().manual_seed(20 + i)) + 0.5).to(td)
+        post = None
+        if i != 2:  # term 2 has no post vector (scale 1)
+            post = (torch.rand(R, generator=torch.Generator().manual_seed(30 + i)) + 0.25).to(td)
+            post[torch.rand(R, generator=torch.Generator().manual_seed(50 + i)) < 0.4] *= -1
+        xs = x[:, :kd].float() if pre is None else (x[:, :kd].float() * pre[:kd].float()).to(td).float()
+        t = xs @ torch.from_numpy(signs).float().t()
+        ref += t if post is None else t * post.float()
+        terms.append((f, x.to(dev), None if pre is None else pre.to(dev), None if post is None else post.to(dev)))
+    bias = None
+    if with_bias:
+        bias = (torch.randn(R, generator=torch.Generator().manual_seed(60)) * 0.1).to(td)
+        ref += bias.float()
+    out = torch.full((m, ld_out), 7.0, dtype=td, device=dev)
+    dbf_ops.sign_gemm(terms, m, R, td, out, ld_out, fill_to=fill_to, bias=None if bias is None else bias.to(dev))
+    o = out.float().cpu()
+    r = _rel(o[:, :R].numpy(), ref.numpy())
+    assert r <= (2e-3 if dtype == "fp16" else 8e-3), r
+    assert torch.all(o[:, R:fill_to] == 0)
+    assert torch.all(o[:, fill_to:] == 7.0)

@@ -364,6 +364,47 @@ def test_gemm_streaming_mid_m_variants(dev, bits, case, plan):
         _gemm_check(dev, _case(768, 80 if bits != 3 else 96, bits, seed=160 + bits), 30, "fp16", bias=True)
 
 
+# The streaming GEMM at 32 < M <= 128 (4 or 8 row blocks per B operand, dequantised B operand) and
+# its K split across workgroups (fp32 partials summed by k_splitk_reduce), forced by plan knobs:
+# splits the planner reduces to an even unit count, a ragged last n-tile, bias, bf16, act-order and
+# groups of 256.  Tolerances are regression bounds well under the 1e-2 contract.
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [33, 64, 100, 128])
+@pytest.mark.parametrize("split", [1, 2, 4])
+def test_gemm_stream_mid_m_split(dev, bits, m, split, plan):
+    plan("OC_GEMM_STREAM", 1)
+    plan("OC_GEMM_STREAM_S", split)
+    n = 720 if bits != 3 else 736
+    _gemm_check(dev, _case(2048, n, bits, seed=400 + 7 * bits + m + split), m, "fp16", bias=(split == 2), tol=2e-3)
+
+
+# The tiled GEMM at the mid M the streaming GEMM now serves (64-row tiles, K split pieces).
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [33, 64, 100])
+def test_gemm_tiled_mid_m(dev, bits, m, plan):
+    plan("OC_GEMM_STREAM", 0)
+    _gemm_check(dev, _case(2048, 720 if bits != 3 else 736, bits, seed=460 + bits + m), m, "fp16", bias=True,
+                tol=2e-3)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("case", ["bf16", "act", "g256", "wide"])
+def test_gemm_stream_mid_m_variants(dev, bits, case, plan):
+    plan("OC_GEMM_STREAM", 1)
+    if case == "bf16":
+        plan("OC_GEMM_STREAM_S", 2)
+        _gemm_check(dev, _case(2048, 512, bits, seed=420 + bits), 96, "bf16", bias=True, tol=8e-3)
+    elif case == "act":
+        plan("OC_GEMM_STREAM_S", 4)
+        _gemm_check(dev, _case(4096, 512, bits, 128, True, seed=430 + bits), 72, "fp16", bias=True, tol=2e-3)
+    elif case == "g256":
+        plan("OC_GEMM_STREAM_S", 2)
+        _gemm_check(dev, _case(4096, 400 if bits != 3 else 416, bits, 256, False, seed=440 + bits), 50, "fp16",
+                    tol=2e-3)
+    else:
+        _gemm_check(dev, _case(1024, 16384, bits, seed=450 + bits), 120, "fp16", tol=2e-3)
+
+
 # The large-M GEMM with K not a multiple of 128: the last k-block's x chunks past K load as zeros
 # through the buffer range check (the padded codes dequantise to -z s, so stale x there would show).
 @pytest.mark.parametrize("bits", BITS)
