@@ -334,11 +334,14 @@ def report_configs(dev, only=None):
             for m in ms:
                 x = synth.activations(m, n_dim, dt, seed=500 + m).to(dev)
                 y = torch.empty_like(x)
-                us = _time_graph(lambda i: ops.hadamard(x, out=y), 1, 64 if m <= 256 else 16)
-                k_blk = ops.hadamard_order(n_dim)
-                fl = 2.0 * m * n_dim * (k_blk + math.log2(n_dim // k_blk))
-                out.append(_entry(cfg, f"hadamard n={n_dim} (K={k_blk})", n_dim, n_dim, m, 0, 4 * m * n_dim, fl, us,
-                                  "fp16" if dt == torch.float16 else "bf16"))
+                # the reference's default rounding (fp32_had=False, pure-PyTorch transform: every
+                # butterfly stage rounded) and the fused-transform-op rounding (one rounding)
+                for rnd in ("stages", "once"):
+                    us = _time_graph(lambda i: ops.hadamard(x, out=y, rounding=rnd), 1, 64 if m <= 256 else 16)
+                    k_blk = ops.hadamard_order(n_dim)
+                    fl = 2.0 * m * n_dim * (k_blk + math.log2(n_dim // k_blk))
+                    out.append(_entry(cfg, f"hadamard n={n_dim} (K={k_blk}) rounding={rnd}", n_dim, n_dim, m, 0,
+                                      4 * m * n_dim, fl, us, "fp16" if dt == torch.float16 else "bf16"))
     # config 3: one DBF path and the two-path MDBF variant, per shape
     for i, (name, k, n) in enumerate(synth.CONFIG3 if only is None or 3 in only else []):
         cases = [synth.dbf_case(name, k, n, 1.0, seed=300 + 2 * i + j) for j in range(2)]

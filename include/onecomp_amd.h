@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 4
+#define OC_ABI_VERSION 5
 
 enum {
   OC_OK = 0,
@@ -42,6 +42,16 @@ enum {
 };
 
 enum { OC_DTYPE_F16 = 0, OC_DTYPE_BF16 = 1 };
+
+/* Rounding points of oc_hadamard, as the reference's apply_online_hadamard
+ * (vllm_plugins/utils/rotation.py:100-112 -> hadamard_utils.py:178-199) rounds:
+ * FP32   fp32_had=True: fp32 throughout, one rounding to the activation dtype;
+ * ONCE   fp32_had=False with the fused transform op (the fast_hadamard_transform
+ *        package): transform rounded once, then the 1/sqrt(n) division, then the
+ *        H_K product (three roundings; two when K = 1);
+ * STAGES fp32_had=False with the reference's pure-PyTorch transform (its default
+ *        install, hadamard_utils.py:26-44): every butterfly stage rounded, then as ONCE. */
+enum { OC_HAD_ROUND_FP32 = 0, OC_HAD_ROUND_ONCE = 1, OC_HAD_ROUND_STAGES = 2 };
 
 /* Zero-point storage of qzeros (gptq_layer.py:543-557; checkpoint.py:217-221). */
 enum {
@@ -261,11 +271,12 @@ int oc_hadamard_order(int n);
 int oc_hadamard_block(int K, int8_t* out);
 
 /* y[m, :] = (H_K (x) H_L) x[m, :] / sqrt(n) with n = K * L, L a power of two, n <= 32768;
- * hadk: device int8 [K * K] from oc_hadamard_block (NULL when K = 1).  fp32 internally, one
- * rounding to act_dtype; y may alias x when ld_y == ld_x.  One kernel on `stream`.
+ * hadk: device int8 [K * K] from oc_hadamard_block (NULL when K = 1).  rounding: OC_HAD_ROUND_*
+ * (above); sqrt(n) is the float32 value, the division an fp32 division.  y may alias x when
+ * ld_y == ld_x.  One kernel on `stream`.
  * Replaces matmul_hadU_cuda (hadamard_utils.py:178-199) as applied to the down_proj input by
  * apply_online_hadamard / RotatedLinearMethod (vllm_plugins/utils/rotation.py:100-112, 146-228). */
-int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* hadk, int K, int act_dtype,
+int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* hadk, int K, int act_dtype, int rounding,
                 void* y, int ld_y, void* stream);
 
 #ifdef __cplusplus

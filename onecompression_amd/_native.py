@@ -51,12 +51,13 @@ SIGNATURES = {
     "oc_sign_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
     "oc_hadamard_order": (c_int, [c_int]),
     "oc_hadamard_block": (c_int, [c_int, P]),
-    "oc_hadamard": (c_int, [P, c_int, c_int, c_int, P, c_int, c_int, P, c_int, P]),
+    "oc_hadamard": (c_int, [P, c_int, c_int, c_int, P, c_int, c_int, c_int, P, c_int, P]),
     "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, c_size_t, P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
+OC_HAD_ROUND_FP32, OC_HAD_ROUND_ONCE, OC_HAD_ROUND_STAGES = 0, 1, 2
 OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2
 ERR_NAMES = {-1: "INVALID", -2: "UNSUPPORTED", -3: "SHAPE", -4: "HIP", -5: "WORKSPACE", -6: "GIDX"}
 OC_ERR_INVALID, OC_ERR_UNSUPPORTED, OC_ERR_SHAPE, OC_ERR_HIP, OC_ERR_WORKSPACE, OC_ERR_GIDX = -1, -2, -3, -4, -5, -6

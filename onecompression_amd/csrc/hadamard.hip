@@ -29,12 +29,24 @@
 // chi is the quadratic character mod q.
 //
 // One kernel, one workgroup per row: the length-L transforms in fp32 in LDS,
-// then u = FWHT / sqrt(n) rounded to the activation dtype and the H_K block
-// mix on MFMA (fp32 accumulation, one more rounding).  With K = 1 the
-// transform is rounded once.  The reference's
-// default fp32_had=False path rounds three times (after the transform, after
-// the 1/sqrt(n) division, after the H_K product); its fp32_had=True path
-// rounds once, and differs from this one by the intermediate rounding.
+// then the 1/sqrt(n) scaling and the H_K block mix on MFMA (fp32
+// accumulation), with the rounding points of the reference
+// (rotation.py:100-112 -> hadamard_utils.py:178-199), by `rounding`:
+//   OC_HAD_ROUND_FP32 (fp32_had = true: x.float() throughout, one cast back):
+//     y = RNE(H_K (U / s)) with U / s kept in fp32: the mix multiplies H_K by
+//     u split into two (fp16) or three (bf16) activation-dtype parts,
+//     hi + lo (+ lo2), each an exact MFMA operand (fp16 lo is stored times
+//     2^11, out of the subnormal range, and its fp32 sums scaled back), so the
+//     fp32 sum carries u to 22 (fp16) / 24 (bf16) bits -- one rounding;
+//   OC_HAD_ROUND_ONCE (fp32_had = false with the fused transform op, which
+//     returns the activation dtype from fp32 sums): u = RNE(RNE(U) / s),
+//     y = RNE(H_K u) -- three roundings (two with K = 1);
+//   OC_HAD_ROUND_STAGES (fp32_had = false with the reference's pure-PyTorch
+//     transform, hadamard_utils.py:26-44, which adds in the activation dtype):
+//     every butterfly stage (bit 0 first, as the reference) rounds, then as
+//     ROUND_ONCE.  Only the one-workgroup-per-row kernel has stages.
+// U is the fp32 length-L transform and s = float32(sqrt(n)), the reference's
+// torch.tensor(n).sqrt(); the divisions are IEEE fp32 divisions.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -195,12 +207,49 @@ __device__ __forceinline__ uint32_t had_pair(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(had_f2{lo, hi}, oc_half2));
 }
 
+// u of one transform value U under the rounding mode (see the top of the
+// file): ROUND_FP32 gives the fp32 U / s, the others the activation-dtype
+// value RNE(RNE(U) / s) as fp32.
+template <bool BF16>
+__device__ __forceinline__ float had_u(float U, float sq, int mode) {
+  return mode == OC_HAD_ROUND_FP32 ? U / sq : had_in<BF16>(had_out<BF16>(had_in<BF16>(had_out<BF16>(U)) / sq));
+}
+// One value rounded to the activation dtype (a butterfly stage of ROUND_STAGES).
+template <bool BF16>
+__device__ __forceinline__ float had_rnd(float v) {
+  return had_in<BF16>(had_out<BF16>(v));
+}
+// Part p of u as an exact activation-dtype operand: p = 0 the rounded value,
+// p = 1, 2 the rounded remainders (ROUND_FP32 only; otherwise u is part 0).
+// fp16's remainder is stored times 2^11 (kept out of the subnormal range,
+// which MFMA operands need not honour); the sums of parts p >= 1 are
+// multiplied by had_lo_scale.
+template <bool BF16>
+__device__ __forceinline__ float had_part(float u, int p) {
+  const float hi = had_rnd<BF16>(u);
+  if (p == 0) return hi;
+  if constexpr (BF16) {
+    const float lo = had_rnd<BF16>(u - hi);  // u - hi is exact, as is (u - hi) - lo
+    return p == 1 ? lo : had_rnd<BF16>((u - hi) - lo);
+  } else {
+    return had_rnd<BF16>((u - hi) * 2048.f);
+  }
+}
+template <bool BF16>
+__device__ __forceinline__ constexpr float had_lo_scale() {
+  return BF16 ? 1.f : 1.f / 2048.f;
+}
+// Operand parts of the H_K mix: 2 (fp16) or 3 (bf16) for ROUND_FP32, else 1.
+__host__ __device__ __forceinline__ int had_parts(int mode, bool bf16) {
+  return mode == OC_HAD_ROUND_FP32 ? (bf16 ? 3 : 2) : 1;
+}
+
 // One radix-2^R pass: butterflies (a, b) -> (a + b, a - b) over bits
 // [b0, b0 + R) of the in-segment index, for every segment of the row at once
 // (the segment index sits above those bits, so one group never straddles two).
 // With b0 >= 6 the 64 lanes of a wave read 64 consecutive words per t: no
 // bank conflicts.
-template <int R>
+template <int R, bool BF16, bool STAGES>
 __device__ __forceinline__ void had_pass(float* f, int n, int b0) {
   const int groups = n >> R;
   for (int g = threadIdx.x; g < groups; g += kHadThreads) {
@@ -214,8 +263,8 @@ __device__ __forceinline__ void had_pass(float* f, int n, int b0) {
       for (int t = 0; t < (1 << R); ++t)
         if (!(t & (1 << s))) {
           const float p = v[t], q = v[t | (1 << s)];
-          v[t] = p + q;
-          v[t | (1 << s)] = p - q;
+          v[t] = STAGES ? had_rnd<BF16>(p + q) : p + q;
+          v[t | (1 << s)] = STAGES ? had_rnd<BF16>(p - q) : p - q;
         }
 #pragma unroll
     for (int t = 0; t < (1 << R); ++t) f[base + (t << b0)] = v[t];
@@ -244,6 +293,7 @@ __device__ __forceinline__ float had_lane_xor(float v) {
 // registers, bits 3-5 across lanes g ^ 1, g ^ 2, g ^ 4.  Every lane whose
 // elements are in the row has its partners in the row too (L >= 16 makes n
 // a multiple of 8 * (partner span)).
+template <bool BF16, bool STAGES>
 __device__ __forceinline__ void had_first_bits(float (&v)[8], int lgL, int lane) {
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
@@ -252,25 +302,36 @@ __device__ __forceinline__ void had_first_bits(float (&v)[8], int lgL, int lane)
       for (int t = 0; t < 8; ++t)
         if (!(t & (1 << b))) {
           const float p = v[t], q = v[t | (1 << b)];
-          v[t] = p + q;
-          v[t | (1 << b)] = p - q;
+          v[t] = STAGES ? had_rnd<BF16>(p + q) : p + q;
+          v[t | (1 << b)] = STAGES ? had_rnd<BF16>(p - q) : p - q;
         }
     }
   }
+  // the lane stages: the partner's value plus or minus this lane's (sg v + partner
+  // is the exact sum or difference, rounded like a butterfly of the stage)
   if (lgL > 3) {
     const float sg = (lane & 1) ? -1.f : 1.f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = fmaf(sg, v[t], had_lane_xor<0>(v[t]));
+    for (int t = 0; t < 8; ++t) {
+      const float r = fmaf(sg, v[t], had_lane_xor<0>(v[t]));
+      v[t] = STAGES ? had_rnd<BF16>(r) : r;
+    }
   }
   if (lgL > 4) {
     const float sg = (lane & 2) ? -1.f : 1.f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = fmaf(sg, v[t], had_lane_xor<1>(v[t]));
+    for (int t = 0; t < 8; ++t) {
+      const float r = fmaf(sg, v[t], had_lane_xor<1>(v[t]));
+      v[t] = STAGES ? had_rnd<BF16>(r) : r;
+    }
   }
   if (lgL > 5) {
     const float sg = (lane & 4) ? -1.f : 1.f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = fmaf(sg, v[t], had_lane_xor<2>(v[t]));
+    for (int t = 0; t < 8; ++t) {
+      const float r = fmaf(sg, v[t], had_lane_xor<2>(v[t]));
+      v[t] = STAGES ? had_rnd<BF16>(r) : r;
+    }
   }
 }
 
@@ -307,15 +368,17 @@ constexpr int kHadPre = 4;  // prefetched 16-byte words of the next row per thre
 //     transform in registers and across lanes; fp32 to LDS;
 //  2. radix passes over the remaining bits in LDS (fp32);
 //  3. K = 1: scale, round, store.  K > 1: per chunk of J columns j, write
-//     u^T[j][c] = round(u[c][j] / sqrt(n)) (zero for c >= K) to LDS and form
+//     the NS operand parts of u^T[j][c] (zero for c >= K) to LDS and form
 //     y[i][j] = sum_c H[i][c] u[c][j] with 16x16x32 MFMA (A = H_K as exact
-//     +-1 halves, staged in LDS once; fp32 accumulate; one rounding).
+//     +-1 halves, staged in LDS once; fp32 accumulate over the parts; one
+//     rounding).
 // A row is read whole before any of it is stored, so y may alias x.
-template <bool BF16>
+template <bool BF16, bool STAGES>
 __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int ld_x, int M, int n, int lgL, int K,
-                                                          const int8_t* __restrict__ hadk, int lgJ, float scale,
-                                                          bool vx, bool vy, bool vy4, uint16_t* y, int ld_y) {
-  extern __shared__ __align__(16) float fbuf[];  // n floats | H_K [KR][US] | u^T [J][US]
+                                                          const int8_t* __restrict__ hadk, int lgJ, float sq,
+                                                          int mode, bool vx, bool vy, bool vy4, uint16_t* y,
+                                                          int ld_y) {
+  extern __shared__ __align__(16) float fbuf[];  // n floats | H_K [KR][US] | u^T parts [NS][J][US]
   const int tid = threadIdx.x;
   const int L = 1 << lgL;
   const int G8 = (n + 7) / 8;
@@ -325,6 +388,7 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
   uint16_t* ut = hs + RT * 16 * US;
   const int lane = tid & 63, wave = tid >> 6, col = lane & 15, kq = lane >> 4;
   const bool pre = vx && G8 <= kHadPre * kHadThreads;
+  const int NS = had_parts(mode, BF16);
 
   if (K > 1) {
     for (int q = tid; q < RT * 16 * (KP / 8); q += kHadThreads) {
@@ -361,7 +425,7 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
         } else {
           had_load8<BF16>(xr, n, gg, vx, v);
         }
-        had_first_bits(v, lgL, lane);
+        had_first_bits<BF16, STAGES>(v, lgL, lane);
         float* fp = fbuf + 8 * gg;
         if (8 * gg + 8 <= n) {
           *(oc_f4*)fp = oc_f4{v[0], v[1], v[2], v[3]};
@@ -388,10 +452,10 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
       const int rem = lgL - b0;
       const int r = (rem + (rem + 3) / 4 - 1) / ((rem + 3) / 4);
       switch (r) {
-        case 1: had_pass<1>(fbuf, n, b0); break;
-        case 2: had_pass<2>(fbuf, n, b0); break;
-        case 3: had_pass<3>(fbuf, n, b0); break;
-        default: had_pass<4>(fbuf, n, b0); break;
+        case 1: had_pass<1, BF16, STAGES>(fbuf, n, b0); break;
+        case 2: had_pass<2, BF16, STAGES>(fbuf, n, b0); break;
+        case 3: had_pass<3, BF16, STAGES>(fbuf, n, b0); break;
+        default: had_pass<4, BF16, STAGES>(fbuf, n, b0); break;
       }
       b0 += r;
       had_sync();
@@ -403,14 +467,14 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
         if (vy) {
           const oc_f4 a = *(const oc_f4*)fp, b = *(const oc_f4*)(fp + 4);
           oc_u4 w;
-          w[0] = had_out<BF16>(a[0] * scale) | ((uint32_t)had_out<BF16>(a[1] * scale) << 16);
-          w[1] = had_out<BF16>(a[2] * scale) | ((uint32_t)had_out<BF16>(a[3] * scale) << 16);
-          w[2] = had_out<BF16>(b[0] * scale) | ((uint32_t)had_out<BF16>(b[1] * scale) << 16);
-          w[3] = had_out<BF16>(b[2] * scale) | ((uint32_t)had_out<BF16>(b[3] * scale) << 16);
+          w[0] = had_pair<BF16>(had_u<BF16>(a[0], sq, mode), had_u<BF16>(a[1], sq, mode));
+          w[1] = had_pair<BF16>(had_u<BF16>(a[2], sq, mode), had_u<BF16>(a[3], sq, mode));
+          w[2] = had_pair<BF16>(had_u<BF16>(b[0], sq, mode), had_u<BF16>(b[1], sq, mode));
+          w[3] = had_pair<BF16>(had_u<BF16>(b[2], sq, mode), had_u<BF16>(b[3], sq, mode));
           *(oc_u4*)(yr + 8 * g) = w;
         } else {
           for (int t = 0; t < 8; ++t)
-            if (8 * g + t < n) yr[8 * g + t] = had_out<BF16>(fp[t] * scale);
+            if (8 * g + t < n) yr[8 * g + t] = had_out<BF16>(had_u<BF16>(fp[t], sq, mode));
         }
       }
     } else {
@@ -421,25 +485,37 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
           float v[8];
           if (c0 + 8 <= K && j < L) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] = fc[t * L] * scale;
+            for (int t = 0; t < 8; ++t) v[t] = had_u<BF16>(fc[t * L], sq, mode);
           } else {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] = (c0 + t < K && j < L) ? fc[t * L] * scale : 0.f;
+            for (int t = 0; t < 8; ++t) v[t] = (c0 + t < K && j < L) ? had_u<BF16>(fc[t * L], sq, mode) : 0.f;
           }
-          *(oc_u4*)(ut + jj * US + c0) = oc_u4{had_pair<BF16>(v[0], v[1]), had_pair<BF16>(v[2], v[3]),
-                                               had_pair<BF16>(v[4], v[5]), had_pair<BF16>(v[6], v[7])};
+          for (int p = 0; p < NS; ++p) {
+            float w[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) w[t] = had_part<BF16>(v[t], p);
+            *(oc_u4*)(ut + (p * J + jj) * US + c0) = oc_u4{had_pair<BF16>(w[0], w[1]), had_pair<BF16>(w[2], w[3]),
+                                                           had_pair<BF16>(w[4], w[5]), had_pair<BF16>(w[6], w[7])};
+          }
         }
         had_sync();
         // y^T = u^T H^T: A = u^T rows j, B = H_K rows i; lane (col, kq) ends
         // with y[i = 16 it + col][j = 16 ct + 4 kq .. + 3], one 8-byte store.
         for (int p = wave; p < (RT << lgCT); p += kHadThreads / 64) {
           const int it = p >> lgCT, ct = p & ((1 << lgCT) - 1);
-          oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
+          oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f}, accl = acc;
           for (int ks = 0; ks < KS; ++ks) {
             const int c0 = ks * 32 + 8 * kq;
-            const oc_u4 av = *(const oc_u4*)(ut + (ct * 16 + col) * US + c0);
             const oc_u4 bv = *(const oc_u4*)(hs + (it * 16 + col) * US + c0);
-            acc = oc_mfma16<BF16>(av, bv, acc);
+            acc = oc_mfma16<BF16>(*(const oc_u4*)(ut + (ct * 16 + col) * US + c0), bv, acc);
+            for (int p = 1; p < NS; ++p) {
+              const oc_u4 av = *(const oc_u4*)(ut + (p * J + ct * 16 + col) * US + c0);
+              accl = oc_mfma16<BF16>(av, bv, accl);
+            }
+          }
+          if (NS > 1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(accl[r], had_lo_scale<BF16>(), acc[r]);
           }
           const int i = it * 16 + col, j = j0 + ct * 16 + 4 * kq;
           if (i < K) {
@@ -466,9 +542,10 @@ __global__ __launch_bounds__(kHadThreads) void k_hadamard(const uint16_t* x, int
 // U[j][c] = sum_l W[j][l] x[c L + l] with W[j][l] = (-1)^popcount(j & l)
 // formed in registers (16x16x32 MFMA, A = W, B = x from LDS, fp32
 // accumulate), the waves taking every fourth 32-deep l-step and adding their
-// sums in LDS; u = round(U / sqrt(n)) then forms y[i L + j] = sum_c H_K[i][c]
-// u[j][c] (a second MFMA, one more rounding): the rounding points of
-// k_hadamard, with L / 16 workgroups per row instead of one.  Needs L >= 16
+// sums in LDS; u (had_u: the rounding mode's value) then forms y[i L + j] =
+// sum_c H_K[i][c] u[j][c] (a second MFMA over u's NS operand parts, one
+// rounding): the rounding points of k_hadamard, with L / 16 workgroups per
+// row instead of one.  Needs L >= 16
 // and y not overlapping x (workgroups of a row read all of it while others
 // store).
 constexpr int kHadMmMaxKT = 11;                     // K <= 176
@@ -476,13 +553,13 @@ constexpr int kHadMmUS = kHadMmMaxKT * 16 + 24;     // LDS row of the u tile (ha
 constexpr int kHadMmMaxN = 32768;                   // row staged whole in LDS
 // LDS: block c of the row at c (L + 8) halves (the 16-B pad keeps the 16 lanes of a B read, one
 // block each, in different banks), the waves' partial sums, the u tile.
-size_t had_mm_lds(int n, int K) {
-  return (size_t)(n + 8 * K) * 2 + (size_t)4 * ((K + 15) / 16) * 256 * 4 + 16 * kHadMmUS * 2;
+size_t had_mm_lds(int n, int K, int NS) {
+  return (size_t)(n + 8 * K) * 2 + (size_t)4 * ((K + 15) / 16) * 256 * 4 + (size_t)NS * 16 * kHadMmUS * 2;
 }
 
 template <int KT, bool BF16>
 __global__ __launch_bounds__(256) void k_hadamard_mm(const uint16_t* __restrict__ x, int ld_x, int n, int L, int K,
-                                                      const int8_t* __restrict__ hadk, float scale,
+                                                      const int8_t* __restrict__ hadk, float sq, int mode,
                                                       uint16_t* __restrict__ y, int ld_y) {
   extern __shared__ __align__(16) uint16_t xsm[];
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
@@ -493,7 +570,8 @@ __global__ __launch_bounds__(256) void k_hadamard_mm(const uint16_t* __restrict_
   uint16_t* yr = y + (size_t)row * ld_y;
   const int G8 = n >> 3, LP = L + 8, lgL = 31 - __builtin_clz(L);
   float* red = (float*)(xsm + K * LP);                  // [4 waves][KT][4][64]
-  uint16_t* ut = (uint16_t*)(red + 4 * KT * 256);       // [16][US]
+  uint16_t* ut = (uint16_t*)(red + 4 * KT * 256);       // [NS][16][US]
+  const int NS = had_parts(mode, BF16);
   // stage the row: 8 chunks of 16 B per thread in flight per batch
   for (int q0 = 0; q0 < G8; q0 += 256 * 8) {
     oc_u4 v[8];
@@ -543,30 +621,38 @@ __global__ __launch_bounds__(256) void k_hadamard_mm(const uint16_t* __restrict_
     const float u = red[e] + red[KT * 256 + e] + red[2 * KT * 256 + e] + red[3 * KT * 256 + e];
     const int ln = e & 63, r = (e >> 6) & 3, ct = e >> 8;
     const int jj = 4 * (ln >> 4) + r, c = 16 * ct + (ln & 15);
+    const float uu = had_u<BF16>(u, sq, mode);
     if (K == 1) {
-      if (c == 0) yr[16 * jt + jj] = had_out<BF16>(u * scale);
+      if (c == 0) yr[16 * jt + jj] = had_out<BF16>(uu);
     } else {
-      ut[jj * US + c] = had_out<BF16>(u * scale);
+      for (int p = 0; p < NS; ++p) ut[(p * 16 + jj) * US + c] = had_out<BF16>(had_part<BF16>(uu, p));
     }
   }
   if (K == 1) return;
   if constexpr (KP > 16 * KT) {  // c in [16 KT, KP): zero
-    for (int q = tid; q < 16 * (KP - 16 * KT); q += 256)
+    for (int q = tid; q < NS * 16 * (KP - 16 * KT); q += 256)
       ut[(q / (KP - 16 * KT)) * US + 16 * KT + q % (KP - 16 * KT)] = 0;
   }
   __syncthreads();
   // y[i][j] = sum_c u[j][c] H[i][c]: A = u rows j, B = H_K rows i (k = c); wave w takes i-tiles w, w + 4, ...
   for (int it = wave; it < KT; it += 4) {
     const int i = 16 * it + col;
-    oc_f4 a2 = oc_f4{0.f, 0.f, 0.f, 0.f};
+    oc_f4 a2 = oc_f4{0.f, 0.f, 0.f, 0.f}, a2l = a2;
 #pragma unroll
     for (int c0 = 0; c0 < KP; c0 += 32) {
       const int cb = c0 + 8 * kq;
-      const oc_u4 uv = *(const oc_u4*)(ut + col * US + cb);
       uint32_t p0 = 0, p1 = 0, p2 = 0, p3 = 0;
       if (i < K && cb < K) had_signs<BF16>(*(const uint32_t*)(hadk + i * K + cb), p0, p1);
       if (i < K && cb + 4 < K) had_signs<BF16>(*(const uint32_t*)(hadk + i * K + cb + 4), p2, p3);
-      a2 = oc_mfma16<BF16>(uv, oc_u4{p0, p1, p2, p3}, a2);
+      a2 = oc_mfma16<BF16>(*(const oc_u4*)(ut + col * US + cb), oc_u4{p0, p1, p2, p3}, a2);
+      for (int p = 1; p < NS; ++p) {
+        const oc_u4 uv = *(const oc_u4*)(ut + (p * 16 + col) * US + cb);
+        a2l = oc_mfma16<BF16>(uv, oc_u4{p0, p1, p2, p3}, a2l);
+      }
+    }
+    if (NS > 1) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a2[r] = fmaf(a2l[r], had_lo_scale<BF16>(), a2[r]);
     }
     // a2[r] = y[i = 16 it + col][j = 16 jt + 4 kq + r]
     if (i < K) {
@@ -578,18 +664,18 @@ __global__ __launch_bounds__(256) void k_hadamard_mm(const uint16_t* __restrict_
 }
 
 // Dynamic LDS of k_hadamard for (n, K) with chunks of J columns.
-size_t had_lds_bytes(int n, int K, int J) {
+size_t had_lds_bytes(int n, int K, int J, int NS) {
   size_t b = (size_t)n * 4;
-  if (K > 1) b += (size_t)(((K + 15) / 16) * 16 + J) * (((K + 31) & ~31) + 8) * 2;
+  if (K > 1) b += (size_t)(((K + 15) / 16) * 16 + NS * J) * (((K + 31) & ~31) + 8) * 2;
   return b;
 }
 
 // log2 of the widest chunk (a power of two, 16 .. max(L, 16)) that fits the
 // LDS; -1 if none does.
-int had_chunk_log2(int n, int K) {
+int had_chunk_log2(int n, int K, int NS) {
   int lg = 4;
   while ((1 << (lg + 1)) <= n / K) ++lg;
-  while (lg >= 4 && had_lds_bytes(n, K, 1 << lg) > kHadMaxLds) --lg;
+  while (lg >= 4 && had_lds_bytes(n, K, 1 << lg, NS) > kHadMaxLds) --lg;
   return lg >= 4 ? lg : -1;
 }
 
@@ -612,7 +698,7 @@ extern "C" int oc_hadamard_block(int K, int8_t* out) {
 }
 
 extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* hadk, int K, int act_dtype,
-                           void* y, int ld_y, void* stream) {
+                           int rounding, void* y, int ld_y, void* stream) {
   OC_REQUIRE(x && y, OC_ERR_INVALID, "null pointer");
   OC_REQUIRE(M >= 0 && n > 0 && ld_x >= n && ld_y >= n, OC_ERR_INVALID, "bad shape M=%d n=%d ld_x=%d ld_y=%d", M,
              n, ld_x, ld_y);
@@ -622,14 +708,18 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
   OC_REQUIRE(K == 1 || hadk, OC_ERR_INVALID, "K=%d needs the K x K block", K);
   OC_REQUIRE(K == 1 || K % 4 == 0, OC_ERR_SHAPE, "Hadamard order K=%d is not a multiple of 4", K);
   OC_REQUIRE(K == 1 || ((uintptr_t)hadk & 3) == 0, OC_ERR_INVALID, "the K x K block must be 4-byte aligned");
-  const int lgJ = K > 1 ? had_chunk_log2(n, K) : 4;
-  const size_t lds = had_lds_bytes(n, K, lgJ >= 4 ? 1 << lgJ : 16);
+  OC_REQUIRE(rounding == OC_HAD_ROUND_FP32 || rounding == OC_HAD_ROUND_ONCE || rounding == OC_HAD_ROUND_STAGES,
+             OC_ERR_INVALID, "bad rounding %d", rounding);
+  const int mode = rounding;
+  const int NS = had_parts(mode, act_dtype == OC_DTYPE_BF16);
+  const int lgJ = K > 1 ? had_chunk_log2(n, K, NS) : 4;
+  const size_t lds = had_lds_bytes(n, K, lgJ >= 4 ? 1 << lgJ : 16, NS);
   OC_REQUIRE(lds <= kHadMaxLds, OC_ERR_UNSUPPORTED, "n=%d (K=%d) needs %zu bytes of LDS, above the %zu of one CU",
              n, K, lds, kHadMaxLds);
   if (M == 0) return 0;
   int lgL = 0;
   while ((1 << lgL) < n / K) ++lgL;
-  const float scale = 1.0f / sqrtf((float)n);
+  const float sq = sqrtf((float)n);  // IEEE-rounded, as torch.tensor(n).sqrt()
   const bool vx = n % 8 == 0 && ld_x % 8 == 0 && ((uintptr_t)x & 15) == 0;
   const bool vy = n % 8 == 0 && ld_y % 8 == 0 && ((uintptr_t)y & 15) == 0;
   const bool vy4 = (n / K) % 4 == 0 && ld_y % 4 == 0 && ((uintptr_t)y & 7) == 0;
@@ -637,22 +727,21 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
   const char *xb = (const char*)x, *yb = (const char*)y;
   const bool overlap = xb < yb + (size_t)M * ld_y * 2 && yb < xb + (size_t)M * ld_x * 2;
   const int mm_max = oc::knob("OC_HAD_MM_M", 16);
-  if (M <= mm_max && Lh >= 16 && K <= 16 * kHadMmMaxKT && n <= kHadMmMaxN && !overlap && vx &&
+  if (mode != OC_HAD_ROUND_STAGES && M <= mm_max && Lh >= 16 && K <= 16 * kHadMmMaxKT && n <= kHadMmMaxN && !overlap && vx &&
       ((uintptr_t)y & 1) == 0) {
     hipStream_t st = (hipStream_t)stream;
-    const float sc = 1.0f / sqrtf((float)n);
     const dim3 grid((unsigned)(M * (Lh / 16)));
-    const size_t mlds = had_mm_lds(n, K);
+    const size_t mlds = had_mm_lds(n, K, NS);
     const int KT = (K + 15) / 16;
     const bool bf = act_dtype == OC_DTYPE_BF16;
 #define OC_HM(KT_)                                                                                              \
   if (KT == KT_) {                                                                                              \
     if (bf)                                                                                                     \
       hipLaunchKernelGGL((k_hadamard_mm<KT_, true>), grid, dim3(256), mlds, st, (const uint16_t*)x, ld_x, n, Lh, K, \
-                         hadk, sc, (uint16_t*)y, ld_y);                                                         \
+                         hadk, sq, mode, (uint16_t*)y, ld_y);                                                   \
     else                                                                                                        \
       hipLaunchKernelGGL((k_hadamard_mm<KT_, false>), grid, dim3(256), mlds, st, (const uint16_t*)x, ld_x, n, Lh,   \
-                         K, hadk, sc, (uint16_t*)y, ld_y);                                                      \
+                         K, hadk, sq, mode, (uint16_t*)y, ld_y);                                                \
   }
     OC_HM(1) OC_HM(2) OC_HM(3) OC_HM(4) OC_HM(5) OC_HM(6) OC_HM(7) OC_HM(8) OC_HM(9) OC_HM(10) OC_HM(11)
 #undef OC_HM
@@ -662,12 +751,18 @@ extern "C" int oc_hadamard(const void* x, int M, int n, int ld_x, const int8_t* 
   const int per_cu = (int)(kHadMaxLds / lds) < 2 ? 1 : 2;
   const int grid = M < oc_device_cus() * per_cu ? M : oc_device_cus() * per_cu;
   hipStream_t st = (hipStream_t)stream;
-  if (act_dtype == OC_DTYPE_BF16)
-    hipLaunchKernelGGL(k_hadamard<true>, dim3(grid), dim3(kHadThreads), lds, st, (const uint16_t*)x, ld_x, M, n,
-                       lgL, K, hadk, lgJ, scale, vx, vy, vy4, (uint16_t*)y, ld_y);
-  else
-    hipLaunchKernelGGL(k_hadamard<false>, dim3(grid), dim3(kHadThreads), lds, st, (const uint16_t*)x, ld_x, M, n,
-                       lgL, K, hadk, lgJ, scale, vx, vy, vy4, (uint16_t*)y, ld_y);
+#define OC_HK(B_, S_)                                                                                       \
+  hipLaunchKernelGGL((k_hadamard<B_, S_>), dim3(grid), dim3(kHadThreads), lds, st, (const uint16_t*)x, ld_x, M, n, \
+                     lgL, K, hadk, lgJ, sq, mode, vx, vy, vy4, (uint16_t*)y, ld_y)
+  const bool stages = mode == OC_HAD_ROUND_STAGES;
+  if (act_dtype == OC_DTYPE_BF16) {
+    if (stages) OC_HK(true, true);
+    else OC_HK(true, false);
+  } else {
+    if (stages) OC_HK(false, true);
+    else OC_HK(false, false);
+  }
+#undef OC_HK
   OC_HIP(hipGetLastError());
   return 0;
 }

@@ -267,8 +267,18 @@ def hadamard_block(k: int, device) -> Optional[torch.Tensor]:
     return t
 
 
-def hadamard(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Online Hadamard of the last axis: (H_K (x) H_L) x / sqrt(n), fp32 inside, one rounding."""
+_HAD_ROUNDING = {"fp32": N.OC_HAD_ROUND_FP32, "once": N.OC_HAD_ROUND_ONCE, "stages": N.OC_HAD_ROUND_STAGES}
+
+
+def hadamard(x: torch.Tensor, out: Optional[torch.Tensor] = None, rounding: str = "stages") -> torch.Tensor:
+    """Online Hadamard of the last axis: (H_K (x) H_L) x / sqrt(n), rounded as the reference's
+    apply_online_hadamard (rotation.py:100-112) rounds: "fp32" for fp32_had=True (one rounding);
+    for fp32_had=False "stages" (the reference's pure-PyTorch transform adds in x's dtype, every
+    butterfly stage rounds; its default install) or "once" (with the fast_hadamard_transform
+    package: the transform rounds once), each followed by the rounded 1/sqrt(n) division and the
+    rounded H_K product."""
+    if rounding not in _HAD_ROUNDING:
+        raise ValueError(f"rounding must be one of {sorted(_HAD_ROUNDING)}, got {rounding!r}")
     if x.dtype not in _DT:
         raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
     n = x.shape[-1]
@@ -285,8 +295,8 @@ def hadamard(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tenso
     lo, hi = x2.data_ptr(), x2.data_ptr() + x2.shape[0] * x2.stride(0) * x2.element_size()
     olo, ohi = out.data_ptr(), out.data_ptr() + out.shape[0] * out.stride(0) * out.element_size()
     dst = torch.empty_like(x2) if (olo < hi and lo < ohi) else out
-    N.call("oc_hadamard", _ptr(x2), x2.shape[0], n, x2.stride(0), _ptr(blk), k, _DT[x.dtype], _ptr(dst),
-           dst.stride(0), _stream(x.device))
+    N.call("oc_hadamard", _ptr(x2), x2.shape[0], n, x2.stride(0), _ptr(blk), k, _DT[x.dtype], _HAD_ROUNDING[rounding],
+           _ptr(dst), dst.stride(0), _stream(x.device))
     if dst is not out:
         out.copy_(dst)
     return out.reshape(x.shape)

@@ -8,12 +8,12 @@ Mirrors vllm_plugins/utils/rotation.py:
   through a forward pre-hook installed at create_weights /
   process_weights_after_loading, as the reference does for tp = 1.  The
   transform is ``ops.hadamard`` (one HIP launch: the length-L transforms in
-  fp32, rounded once to the activation dtype, then the K x K mix on MFMA with
-  fp32 accumulation and one more rounding; up to 16 rows as products over
-  L / 16 workgroups per row, from 32 rows one workgroup per row).  The reference's default
-  ``fp32_had=False`` rounds three times (transform, 1/sqrt(n), H_K product);
-  ``fp32_had=True`` rounds once, and this result differs from it by the one
-  intermediate rounding;
+  fp32, then the K x K mix on MFMA with fp32 accumulation; up to 16 rows as
+  products over L / 16 workgroups per row, from 32 rows one workgroup per
+  row), rounded as the metadata's ``fp32_had`` asks: True keeps fp32 and
+  rounds once; False (the default) rounds every butterfly stage (the
+  reference's pure-PyTorch transform; once with FAST_HADAMARD_TRANSFORM),
+  the 1/sqrt(n) division and the H_K product;
 - ``maybe_wrap_rotation_method`` (:242-261).
 Tensor parallelism > 1 needs an all-gather of the input first (:179-195);
 this one-GPU build raises for it.
@@ -48,16 +48,22 @@ class RotationMetadata:
         return self.rotated and is_online_hadamard_target(prefix)
 
 
+# The reference's transform op is the fast_hadamard_transform package when it is installed,
+# else its pure-PyTorch butterflies (hadamard_utils.py:17-68); its dependencies do not include the
+# package, so fp32_had=False follows the butterflies' per-stage rounding unless this is set.
+FAST_HADAMARD_TRANSFORM = False
+
+
 def apply_online_hadamard(x, *, fp32_had: bool = False, cache_owner: Any = None):
     """Online Hadamard of the last axis (rotation.py:100-112); the block order is cached on the owner."""
     from . import ops
 
-    del fp32_had  # one arithmetic for both settings (see the module docstring)
     if cache_owner is not None:
         cached = getattr(cache_owner, "_onecomp_hadamard_cache", None)
         if cached is None or cached[0] != x.shape[-1]:
             setattr(cache_owner, "_onecomp_hadamard_cache", (x.shape[-1], ops.hadamard_order(x.shape[-1])))
-    return ops.hadamard(x)
+    rounding = "fp32" if fp32_had else ("once" if FAST_HADAMARD_TRANSFORM else "stages")
+    return ops.hadamard(x, rounding=rounding)
 
 
 def make_hadamard_forward_pre_hook(*, fp32_had: bool):

@@ -16,6 +16,18 @@ module, as the checker.  The product path is onecompression_amd/csrc/hadamard.hi
   2m).  Pinned by the closed form H[i, j] = (-1)^popcount(i & j).
 - ``online_hadamard``: matmul_hadU_cuda (hadamard_utils.py:178-199) as used by
   apply_online_hadamard (vllm_plugins/utils/rotation.py:100-112), in float64.
+- ``fwht_staged`` / ``online_hadamard_rounded``: the same with the rounding
+  points of apply_online_hadamard: fp32_had=True runs matmul_hadU_cuda on
+  x.float() (transform and division in float32, the product summed exactly
+  from the float32 values) and rounds once in ``.to(x_dtype)`` ('fp32');
+  fp32_had=False runs it in the activation dtype: the transform rounds every
+  butterfly stage with the reference's pure-PyTorch op ('stages'; its
+  default install) or once with the fast_hadamard_transform package
+  ('once'; sums taken exact), the division by torch.tensor(n).sqrt() (a
+  float32 value) rounds, and the H_K matmul (fp32 accumulation, exact here)
+  rounds.  Pinned by hand-derived known answers where the three differ and
+  by the float64 form within the roundings' bound
+  (tests/test_oracle_hadamard.py).
 """
 
 from __future__ import annotations
@@ -132,6 +144,57 @@ def fwht(x: np.ndarray) -> np.ndarray:
         out = v.reshape(*out.shape[:-1], n)
         m *= 2
     return out
+
+
+def _round(v: np.ndarray, dtype: str) -> np.ndarray:
+    """RNE of float values to the activation dtype, returned as float64 values."""
+    if dtype == "fp16":
+        return np.asarray(v, dtype=np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+    # bf16: round the float32 value (the values here are float32-exact or float32 results)
+    u = np.ascontiguousarray(np.asarray(v, dtype=np.float64).astype(np.float32)).view(np.uint32).astype(np.uint64)
+    b = ((u + (((u >> 16) & 1) + 0x7FFF)) >> 16).astype(np.uint32) << 16
+    return b.view(np.float32).astype(np.float64)
+
+
+def fwht_staged(x: np.ndarray, dtype: str) -> np.ndarray:
+    """hadamard_utils.py:26-44 run in the activation dtype: every stage's sums and differences
+    rounded (bit 0 first, as the reference's loop over m = 1, 2, 4, ...)."""
+    out = _round(np.asarray(x, dtype=np.float64), dtype)
+    n = out.shape[-1]
+    m = 1
+    while m < n:
+        v = out.reshape(*out.shape[:-1], n // (2 * m), 2 * m)
+        left, right = v[..., :m].copy(), v[..., m:].copy()
+        v[..., :m] = _round(left + right, dtype)
+        v[..., m:] = _round(left - right, dtype)
+        out = v.reshape(*out.shape[:-1], n)
+        m *= 2
+    return out
+
+
+def online_hadamard_rounded(x: np.ndarray, dtype: str, rounding: str = "stages") -> np.ndarray:
+    """apply_online_hadamard (rotation.py:100-112 -> hadamard_utils.py:178-199) with its roundings.
+
+    x: activation values [M, n] (exactly representable in ``dtype``, 'fp16' or 'bf16'); rounding:
+    'fp32' (fp32_had=True), 'once' (fp32_had=False, fused transform op), 'stages' (fp32_had=False,
+    the pure-PyTorch transform).  Returns the output values as float64.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    n = x.shape[-1]
+    K = pick_order(n)
+    s32 = np.float32(np.sqrt(np.float32(n)))  # torch.tensor(n).sqrt(): float32
+    xv = x.reshape(-1, K, n // K)
+    if rounding == "fp32":
+        u = (fwht(xv).astype(np.float32) / s32).astype(np.float64)
+    elif rounding == "once":
+        u = _round(_round(fwht(xv), dtype).astype(np.float32) / s32, dtype)
+    elif rounding == "stages":
+        u = _round(fwht_staged(xv, dtype).astype(np.float32) / s32, dtype)
+    else:
+        raise ValueError(f"rounding {rounding!r}")
+    if K > 1:
+        u = np.einsum("ic,mcj->mij", hadamard_block(K).astype(np.float64), u)
+    return _round(u, dtype).reshape(x.shape)
 
 
 def online_hadamard(x: np.ndarray) -> np.ndarray:

@@ -65,8 +65,10 @@ def test_dbf_and_mdbf_graph(dev, m):
              lambda b: dbf_ops.mdbf_forward(b[0], [path]))
 
 
-def test_hadamard_graph(dev):
-    _replays(dev, lambda i: [synth.activations(3, 14336, torch.float16, seed=80 + i)], lambda b: ops.hadamard(b[0]))
+@pytest.mark.parametrize("rounding", ["stages", "once", "fp32"])
+def test_hadamard_graph(dev, rounding):
+    _replays(dev, lambda i: [synth.activations(3, 14336, torch.float16, seed=80 + i)],
+             lambda b: ops.hadamard(b[0], rounding=rounding))
 
 
 @pytest.mark.parametrize("m", [1, 6, 100])

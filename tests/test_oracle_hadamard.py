@@ -116,3 +116,46 @@ def test_c_abi_blocks_and_orders_match_oracle():
     for n in (14336, 12288, 17408, 11008, 4096, 640, 25600, 6656, 9984):
         assert lib.oc_hadamard_order(n) == oh.pick_order(n)
     assert lib.oc_hadamard_order(1000) == 0
+
+
+# The reference's rounding points (rotation.py:100-112 -> hadamard_utils.py:26-44, :178-199), pinned
+# by answers derived by hand: fp16 [2048, 1, 1, 1] (n = 4, K = 1, sqrt = 2).  Pure-PyTorch stages:
+# bit 0: [2048 + 1 -> 2048 (tie to even), 2047, 2, 0]; bit 1: [2050, 2047, 2046, 2047]; / 2.
+# Fused op: the exact 2051 rounds to 2052, / 2 = 1026.  fp32: 2051 / 2 = 1025.5 -> 1026 (tie, even).
+def test_rounded_known_answers_fp16():
+    x = np.array([[2048, 1, 1, 1]], dtype=np.float64)
+    assert oh.online_hadamard_rounded(x, "fp16", "stages").tolist() == [[1025, 1023.5, 1023, 1023.5]]
+    assert oh.online_hadamard_rounded(x, "fp16", "once").tolist() == [[1026, 1023.5, 1023.5, 1023.5]]
+    assert oh.online_hadamard_rounded(x, "fp16", "fp32").tolist() == [[1026, 1023.5, 1023.5, 1023.5]]
+
+
+def test_rounded_known_answers_bf16():
+    # bf16 spacing 2 at 256: 256 + 1 -> 256; the exact 259 -> 260; 259 / 2 = 129.5 -> 130
+    x = np.array([[256, 1, 1, 1]], dtype=np.float64)
+    assert oh.online_hadamard_rounded(x, "bf16", "stages").tolist() == [[129, 127.5, 127, 127.5]]
+    assert oh.online_hadamard_rounded(x, "bf16", "once").tolist() == [[130, 127.5, 127.5, 127.5]]
+    assert oh.online_hadamard_rounded(x, "bf16", "fp32").tolist() == [[130, 127.5, 127.5, 127.5]]
+
+
+def test_rounded_stage_order_planted():
+    """Stages taken high bit first (a plausible mistake) change the known answer above."""
+    x = np.array([[2048, 1, 1, 1]], dtype=np.float64)
+    v = x.copy()
+    for m in (2, 1):  # reversed
+        w = v.reshape(1, 4 // (2 * m), 2 * m)
+        left, right = w[..., :m].copy(), w[..., m:].copy()
+        w[..., :m] = oh._round(left + right, "fp16")
+        w[..., m:] = oh._round(left - right, "fp16")
+        v = w.reshape(1, 4)
+    wrong = oh._round(v.astype(np.float32) / np.float32(2), "fp16")
+    assert wrong.tolist() != oh.online_hadamard_rounded(x, "fp16", "stages").tolist()
+
+
+@pytest.mark.parametrize("n", [4096, 14336, 12288, 11008])
+@pytest.mark.parametrize("rounding,tol", [("fp32", 1e-3), ("once", 2e-3), ("stages", 1e-2)])
+def test_rounded_near_float64(n, rounding, tol):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((2, n)).astype(np.float16).astype(np.float64)
+    ref = oh.online_hadamard(x)
+    got = oh.online_hadamard_rounded(x, "fp16", rounding)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) <= tol
