@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 5
+#define OC_ABI_VERSION 6
 
 enum {
   OC_OK = 0,
@@ -183,11 +183,12 @@ int oc_gptq_gemm_grouped(const void* x, int M, int K, const oc_gptq_part* parts,
 
 /* ---------------------------------------------------------------- MoE experts -------------- */
 
-/* Workspace bytes oc_moe_gptq_forward needs (host only). */
-size_t oc_moe_workspace_bytes(int M, int H, int I, int topk);
+/* Workspace bytes oc_moe_gptq_forward needs (host only); act_order != 0 when perm13 or perm2 is
+ * passed. */
+size_t oc_moe_workspace_bytes(int M, int H, int I, int topk, int act_order);
 
-/* Mixture-of-experts block with GPTQ experts (all experts share bits and group size, no
- * act-order).  For token t < M and slot j < topk, pair p = t * topk + j runs expert e = ids[p]
+/* Mixture-of-experts block with GPTQ experts (all experts share bits and group size).  For token
+ * t < M and slot j < topk, pair p = t * topk + j runs expert e = ids[p]
  * (int32; ids outside [0, E) contribute nothing):
  *   gate|up = x[t] @ W13_e^T (+ b13_e),  h = act(gate, up),  y[t] += weights[p] * (h @ W2_e^T + b2_e)
  * act: 0 = SiLU(gate) * up, 1 = GELU-tanh(gate) * up, 2 = the gpt-oss combine
@@ -196,6 +197,10 @@ size_t oc_moe_workspace_bytes(int M, int H, int I, int topk);
  * w13: E experts' oc_gptq_prepare output for the merged gate|up layer (H -> 2I, gate columns
  * first), w13_stride bytes apart; meta13 their scale/zero words, meta13_stride words apart; b13
  * [E, 2I] or NULL.  w2 / meta2 / b2 likewise for down (I -> H).  x [M, H], y [M, H] in act_dtype.
+ * Act-order experts: perm13 [E, H] / perm2 [E, I] int32 are each expert's oc_gptq_prepare
+ * permutation of gate|up (gate and up share one g_idx) / down, or NULL for experts in checkpoint
+ * order; x and h are then gathered per pair in that order (one more launch each), and the
+ * grouped-GEMM prefill path is not used.
  * Three launches on `stream` (gate|up with the activation, down, the top-k sum), no host
  * synchronisation, no allocation.  Pairs that share an expert share one read of its weights,
  * up to 16 at a time; beyond 64 pairs a fourth launch first sorts the pairs by expert
@@ -208,9 +213,9 @@ size_t oc_moe_workspace_bytes(int M, int H, int I, int topk);
 int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, int topk, const int32_t* ids,
                         const float* weights, const void* w13, size_t w13_stride, const uint32_t* meta13,
                         size_t meta13_stride, const void* b13, const void* w2, size_t w2_stride,
-                        const uint32_t* meta2, size_t meta2_stride, const void* b2, int bits,
-                        int group_size, int act, float alpha, float limit, int act_dtype, void* y,
-                        void* workspace, size_t ws_bytes, void* stream);
+                        const uint32_t* meta2, size_t meta2_stride, const void* b2, const int32_t* perm13,
+                        const int32_t* perm2, int bits, int group_size, int act, float alpha, float limit,
+                        int act_dtype, void* y, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------- DBF / MDBF ---------------- */
 

@@ -41,9 +41,9 @@ SIGNATURES = {
     "oc_gptq_noalloc_scratch_bytes": (c_size_t, []),
     "oc_gptq_grouped_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
     "oc_gptq_gemm_grouped": (c_int, [P, c_int, c_int, P, c_int, c_int, P, c_int, P, c_size_t, P]),
-    "oc_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "oc_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "oc_moe_gptq_forward": (c_int, [P, c_int, c_int, c_int, c_int, c_int, P, P, P, c_size_t, P, c_size_t,
-                                    P, P, c_size_t, P, c_size_t, P, c_int, c_int, c_int, ctypes.c_float,
+                                    P, P, c_size_t, P, c_size_t, P, P, P, c_int, c_int, c_int, ctypes.c_float,
                                     ctypes.c_float, c_int, P, P, c_size_t, P]),
     "oc_dbf_layout": (c_int, [c_int, c_int, c_size_t_p, c_int_p, c_int_p]),
     "oc_dbf_unpack_signs": (c_int, [P, c_int, c_int, P, P]),
@@ -55,7 +55,7 @@ SIGNATURES = {
     "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, c_size_t, P]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
 OC_HAD_ROUND_FP32, OC_HAD_ROUND_ONCE, OC_HAD_ROUND_STAGES = 0, 1, 2
 OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2

@@ -362,6 +362,7 @@ struct MoeArgs {
   uint16_t* out;        // gate|up launch: h [pairs, I]
   float* part;          // down launch: fp32 sums per pair [pairs, N_pad]
   int pairs, topk, E;
+  int xdiv;             // gate|up: x row of pair p = p / xdiv (topk: token rows; 1: rows gathered per pair)
   int ntiles;           // workgroups per pair: I / 16 (gate|up) or NT(H) (down)
   int I;                // intermediate size
   int act;
@@ -470,7 +471,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_gate_up(const MoeArgs g) {
   a.w = g.base.w + (size_t)r.e * g.w_stride;
   a.meta = g.base.meta + (size_t)r.e * g.meta_stride;
   int xo[XCH];
-  moe_xrows<BITS, XCH, RM>(g, r, p, g.topk, a.K, r.rows, xo);
+  moe_xrows<BITS, XCH, RM>(g, r, p, g.xdiv, a.K, r.rows, xo);
   const int nt[2] = {j, g.ntiles + j};
   oc_f4 yacc[2];
   gemv_accum<BITS, 2, CS, D, W, XCH, BF16>(a, nt, 0, a.NU, r.rows, [&](int q, int) { return a.x + xo[q]; },
@@ -618,6 +619,20 @@ __global__ __launch_bounds__(256) void k_moe_gather_x(const uint16_t* __restrict
   const uint16_t* src = x + (size_t)(sorted[i] / topk) * H;
   for (int c = threadIdx.x; c < H / 8; c += 256)
     *(oc_u4*)(xs + (size_t)i * H + 8 * c) = *(const oc_u4*)(src + 8 * c);
+}
+
+// Act-order experts (weights stored in each expert's sorted-k order): dst[p, k] =
+// src[(p / div) K + perm[e K + k]] with e = ids[p], zero for pairs without an expert.
+__global__ __launch_bounds__(256) void k_moe_gather_perm(const uint16_t* __restrict__ src, int div, int K,
+                                                         const int32_t* __restrict__ perm,
+                                                         const int32_t* __restrict__ ids, int E,
+                                                         uint16_t* __restrict__ dst) {
+  const int p = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= K) return;
+  const int e = ids[p];
+  uint16_t v = 0;
+  if (e >= 0 && e < E) v = src[(size_t)(p / div) * K + perm[(size_t)e * K + k]];
+  dst[(size_t)p * K + k] = v;
 }
 
 // Prefill path: h = act(gate, up) for the sorted rows (gate|up rounded, bias included).
@@ -2131,13 +2146,13 @@ struct MoeD {  // units in flight per wave
 };
 
 struct MoePlan {
-  size_t h_off, part_off, sorted_off, runs_off, nruns_off, bytes;
+  size_t h_off, part_off, sorted_off, runs_off, nruns_off, xp_off, hp_off, bytes;
   size_t g_sorted, g_pos, g_runs, g_counts, g_xs, g_h13, g_h, g_ys;
   int rm, w1, w2;
   size_t lds1, lds2;
 };
 
-MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
+MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2, bool act_order = false) {
   MoePlan p;
   const size_t pairs = (size_t)M * topk;
   const int h_pad = (H + 15) / 16 * 16;
@@ -2147,6 +2162,13 @@ MoePlan plan_moe(int M, int H, int I, int E, int topk, int bits, int gs2) {
   p.runs_off = p.sorted_off + align256(pairs * 4);
   p.nruns_off = p.runs_off + align256(pairs * 16);
   p.bytes = p.nruns_off + 256;
+  // act-order: x gathered per pair in each expert's k order, and h likewise for down
+  p.xp_off = p.hp_off = 0;
+  if (act_order) {
+    p.xp_off = p.bytes;
+    p.hp_off = p.xp_off + align256(pairs * H * 2);
+    p.bytes = p.hp_off + align256(pairs * I * 2);
+  }
   // prefill path (its buffers reuse the workspace from 0): sorted, pos, runs, counts, then
   // x, gate|up, h and the down outputs in sorted row order
   p.g_sorted = 0;
@@ -2330,17 +2352,18 @@ int moe_prefill(const void* x, int M, int H, int I, int E, int topk, const int32
 
 }  // namespace
 
-extern "C" size_t oc_moe_workspace_bytes(int M, int H, int I, int topk) {
+extern "C" size_t oc_moe_workspace_bytes(int M, int H, int I, int topk, int act_order) {
   if (M <= 0 || H <= 0 || I <= 0 || topk <= 0) return 0;
-  return plan_moe(M, H, I, 1, topk, 4, 128).bytes;
+  return plan_moe(M, H, I, 1, topk, 4, 128, act_order != 0).bytes;
 }
 
 extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, int topk, const int32_t* ids,
                                    const float* weights, const void* w13, size_t w13_stride, const uint32_t* meta13,
                                    size_t meta13_stride, const void* b13, const void* w2, size_t w2_stride,
-                                   const uint32_t* meta2, size_t meta2_stride, const void* b2, int bits,
-                                   int group_size, int act, float alpha, float limit, int act_dtype, void* y,
-                                   void* workspace, size_t ws_bytes, void* stream) {
+                                   const uint32_t* meta2, size_t meta2_stride, const void* b2,
+                                   const int32_t* perm13, const int32_t* perm2, int bits, int group_size, int act,
+                                   float alpha, float limit, int act_dtype, void* y, void* workspace,
+                                   size_t ws_bytes, void* stream) {
   OC_REQUIRE(x && ids && weights && w13 && meta13 && w2 && meta2 && y, OC_ERR_INVALID, "null pointer");
   OC_REQUIRE(bits == 2 || bits == 3 || bits == 4 || bits == 8, OC_ERR_UNSUPPORTED, "unsupported bits=%d", bits);
   OC_REQUIRE(M >= 0 && H > 0 && I > 0 && E > 0 && topk > 0 && topk <= 64, OC_ERR_INVALID,
@@ -2354,7 +2377,8 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
              OC_ERR_SHAPE, "M=%d x topk=%d is too large for one launch", M, topk);
   const int gs13 = oc::eff_group(group_size, H), gs2 = oc::eff_group(group_size, I);
   OC_REQUIRE(gs13 % 32 == 0 && gs2 % 32 == 0, OC_ERR_UNSUPPORTED, "group_size=%d", group_size);
-  const MoePlan mp = plan_moe(M, H, I, E, topk, bits, gs2);
+  const bool act_order = perm13 != nullptr || perm2 != nullptr;
+  const MoePlan mp = plan_moe(M, H, I, E, topk, bits, gs2, act_order);
   OC_REQUIRE(ws_bytes >= mp.bytes && workspace, OC_ERR_WORKSPACE,
              "workspace of %zu bytes is smaller than the %zu required", ws_bytes, mp.bytes);
   const oc::Layout L13 = oc::make_layout(bits, H, 2 * I), L2 = oc::make_layout(bits, I, H);
@@ -2387,7 +2411,7 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   // default serves every size on the sorted-run GEMV path.
   {
     const int gm = oc::knob("OC_MOE_GEMM", 0);
-    if (E <= kMoeMaxE && pairs >= 32 && gm == 1)
+    if (E <= kMoeMaxE && pairs >= 32 && gm == 1 && !act_order)
       return moe_prefill(x, M, H, I, E, topk, ids, weights, w13, w13_stride, meta13, meta13_stride, b13, w2,
                          w2_stride, meta2, meta2_stride, b2, bits, gs13, gs2, act, alpha, limit, bf16, y, ws, mp, st);
   }
@@ -2416,9 +2440,18 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   g.alpha = alpha;
   g.limit = limit;
   uint16_t* h = (uint16_t*)(ws + mp.h_off);
-  // 1. gate | up and the activation
+  // 1. gate | up and the activation (act-order: x gathered per pair in the expert's k order)
   fill(g.base, L13, H, 2 * I, gs13, G13);
   g.base.x = (const uint16_t*)x;
+  g.xdiv = topk;
+  if (perm13) {
+    uint16_t* xp = (uint16_t*)(ws + mp.xp_off);
+    hipLaunchKernelGGL(k_moe_gather_perm, dim3((H + 255) / 256, pairs), dim3(256), 0, st, (const uint16_t*)x, topk,
+                       H, perm13, ids, E, xp);
+    OC_HIP(hipGetLastError());
+    g.base.x = xp;
+    g.xdiv = 1;
+  }
   g.base.w = (const uint8_t*)w13;
   g.base.meta = meta13;
   g.bias = (const uint16_t*)b13;
@@ -2431,9 +2464,16 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
   int rc = bf16 ? launch_moe<true, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, groups * g.ntiles, st)
                 : launch_moe<false, true>(g, bits, cs13, mp.w1, mp.rm, mp.lds1, groups * g.ntiles, st);
   if (rc) return rc;
-  // 2. down per run, fp32 sums per pair
+  // 2. down per run, fp32 sums per pair (act-order: h gathered in the expert's k order)
   fill(g.base, L2, I, H, gs2, G2);
   g.base.x = h;
+  if (perm2) {
+    uint16_t* hp = (uint16_t*)(ws + mp.hp_off);
+    hipLaunchKernelGGL(k_moe_gather_perm, dim3((I + 255) / 256, pairs), dim3(256), 0, st, (const uint16_t*)h, 1, I,
+                       perm2, ids, E, hp);
+    OC_HIP(hipGetLastError());
+    g.base.x = hp;
+  }
   g.base.w = (const uint8_t*)w2;
   g.base.meta = meta2;
   g.bias = nullptr;

@@ -343,14 +343,15 @@ class GPTQMoEMethod(QuantizeMethodBase):
     ``w2_bias`` [E, H].  The loader takes FusedMoE's ``(param, loaded, weight_name, shard_id,
     expert_id)`` with shard_id ``w1`` (gate), ``w3`` (up) or ``w2`` (down).  After loading the
     experts are repacked once (``moe.prepare_experts_merged``) and the checkpoint tensors freed;
-    ``apply`` runs ``oc_moe_gptq_forward``.
+    ``apply`` runs ``oc_moe_gptq_forward``.  With ``desc_act`` the experts' act-order g_idx are
+    registered as ``w13_g_idx`` [E, H] (gate and up load into one row per expert and must agree:
+    the merged gate|up layer has one k order) and ``w2_g_idx`` [E, I].  ``apply_router_weight_on_input``
+    (top-1) scales the input rows by the router weight before the experts.
     """
 
     _ACT = {"silu": "silu", "swigluoai": "gpt_oss", "gelu": "gelu_pytorch_tanh"}
 
     def __init__(self, quant_config: GPTQLayerConfig):
-        if quant_config.desc_act:
-            raise NotImplementedError("act-order (desc_act) MoE experts are not supported")
         self.quant_config = quant_config
 
     def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
@@ -376,6 +377,9 @@ class GPTQMoEMethod(QuantizeMethodBase):
         if getattr(layer, "has_bias", False):
             shapes["w13_bias"] = ((E, 2 * I), params_dtype)
             shapes["w2_bias"] = ((E, H), params_dtype)
+        if cfg.desc_act:
+            shapes["w13_g_idx"] = ((E, H), torch.int32)
+            shapes["w2_g_idx"] = ((E, I), torch.int32)
         for name, (shape, dtype) in shapes.items():
             param = torch.nn.Parameter(torch.zeros(shape, dtype=dtype), requires_grad=False)
             layer.register_parameter(name, param)
@@ -385,8 +389,28 @@ class GPTQMoEMethod(QuantizeMethodBase):
     @staticmethod
     def _load(param, loaded_weight: torch.Tensor, weight_name: str, shard_id: str, expert_id: int,
               return_success: bool = False):
-        """Place one expert's gate (w1) / up (w3) half of a w13 tensor, or its down (w2) tensor."""
+        """Place one expert's gate (w1) / up (w3) half of a w13 tensor, or its down (w2) tensor; a
+        g_idx row (act-order) is shared by w1 and w3, which must agree."""
         dst = param.data[expert_id]
+        if "g_idx" in weight_name:
+            if shard_id not in ("w1", "w3", "w2") or (shard_id == "w2") != ("w2" in weight_name):
+                raise ValueError(f"{weight_name}: unexpected shard_id {shard_id!r}")
+            if tuple(loaded_weight.shape) != tuple(dst.shape):
+                raise ValueError(f"{weight_name} expert {expert_id} shard {shard_id}: checkpoint shape "
+                                 f"{tuple(loaded_weight.shape)} != {tuple(dst.shape)}")
+            g = loaded_weight.to(device=dst.device, dtype=dst.dtype)
+            seen = getattr(param, "_oc_g_idx_seen", None)
+            if seen is None:
+                seen = {}
+                param._oc_g_idx_seen = seen
+            other = seen.get((expert_id, "w3" if shard_id == "w1" else "w1")) if shard_id != "w2" else None
+            if other is not None and not torch.equal(other, g):
+                raise ValueError(f"expert {expert_id}: act-order gate_proj and up_proj g_idx differ; the merged "
+                                 "gate|up layer needs one k order")
+            if shard_id != "w2":
+                seen[(expert_id, shard_id)] = g
+            dst.copy_(g)
+            return True if return_success else None
         if "w13" in weight_name:
             if shard_id not in ("w1", "w3"):
                 raise ValueError(f"{weight_name}: shard_id must be w1 or w3, got {shard_id!r}")
@@ -408,10 +432,15 @@ class GPTQMoEMethod(QuantizeMethodBase):
             raise RuntimeError("GPTQMoEMethod needs the layer on a HIP device before process_weights_after_loading")
         b13 = getattr(layer, "w13_bias", None)
         b2 = getattr(layer, "w2_bias", None)
+        g13 = getattr(layer, "w13_g_idx", None)
+        g2 = getattr(layer, "w2_g_idx", None)
         layer._oc_experts = moe.prepare_experts_merged(
             layer.w13_qweight.data, layer.w13_qzeros.data, layer.w13_scales.data, layer.w2_qweight.data,
             layer.w2_qzeros.data, layer.w2_scales.data, cfg.weight_bits, cfg.group_size, cfg.zero_format,
-            None if b13 is None else b13.data, None if b2 is None else b2.data)
+            None if b13 is None else b13.data, None if b2 is None else b2.data,
+            None if g13 is None else g13.data, None if g2 is None else g2.data)
+        if g13 is not None:
+            g13._oc_g_idx_seen = None
         for name in ("w13_qweight", "w13_qzeros", "w13_scales", "w2_qweight", "w2_qzeros", "w2_scales"):
             getattr(layer, name).data = torch.empty(0, dtype=getattr(layer, name).dtype,
                                                     device=layer.w13_qweight.device)
@@ -423,14 +452,13 @@ class GPTQMoEMethod(QuantizeMethodBase):
         ex = getattr(layer, "_oc_experts", None)
         if ex is None:
             raise RuntimeError("GPTQ MoE layer used before process_weights_after_loading")
-        if getattr(layer, "apply_router_weight_on_input", False):
-            raise NotImplementedError("apply_router_weight_on_input is not supported")
         if getattr(layer, "expert_map", None) is not None:
             raise NotImplementedError("expert parallelism (expert_map) is not supported")
         act = str(getattr(layer, "activation", "silu")).lower().rsplit(".", 1)[-1]
         if act not in self._ACT:
             raise NotImplementedError(f"MoE activation {act!r}; supported: {sorted(self._ACT)}")
-        return moe.moe_forward(x, topk_ids, topk_weights, ex, self._ACT[act])
+        return moe.moe_forward(x, topk_ids, topk_weights, ex, self._ACT[act],
+                               router_weight_on_input=bool(getattr(layer, "apply_router_weight_on_input", False)))
 
 
 @register_quantization_config("mixed_gptq")

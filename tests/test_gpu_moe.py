@@ -316,3 +316,87 @@ def test_moe_per_channel_groups(dev, plan, m, gemm):
     want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "gpt_oss")
     err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
     assert err <= 1e-2, err
+
+
+def _build_act_order(E, H, I, bits, gs, dtype, seed):
+    """Act-order experts: gate and up share one g_idx per expert (one k order for the merged
+    gate|up layer), down has its own; the oracle dequantises with each g_idx."""
+    cases, ref = [], []
+    for e in range(E):
+        g = synth.gptq_case("g", H, I, bits, gs, True, seed=seed + 3 * e)
+        u = synth.gptq_case("u", H, I, bits, gs, False, seed=seed + 3 * e + 1)
+        u.g_idx, u.act_order = g.g_idx.clone(), True
+        d = synth.gptq_case("d", I, H, bits, gs, True, seed=seed + 3 * e + 2)
+        for c in (g, u, d):
+            c.scales = (c.scales.float() * (4.0 / (1 << bits))).to(torch.float16)
+
+        def w32(c):
+            w = og.dequantize(_np(c.qweight), _np(c.qzeros), _np(c.scales), _np(c.g_idx), c.bits, "gptq", dtype)
+            return og.to_f32(w, dtype)
+        cases.append((g, u, d))
+        ref.append({"gate": w32(g), "up": w32(u), "down": w32(d)})
+    return cases, ref
+
+
+@pytest.mark.parametrize("bits", [3, 4, 8])
+@pytest.mark.parametrize("m", [1, 5, 40, 130])  # one row per pair, runs of 4 / 16, sorted runs
+def test_moe_act_order_experts(dev, bits, m):
+    E, H, I, k, gs = 6, 512, 256, 2, 128
+    cases, ref = _build_act_order(E, H, I, bits, gs, "fp16", seed=500 + bits)
+    dv = lambda c: (c.qweight.to(dev), c.qzeros.to(dev), c.scales.to(dev), c.g_idx.to(dev))  # noqa: E731
+    ex = moe.prepare_experts([dv(g) for g, _, _ in cases], [dv(u) for _, u, _ in cases],
+                             [dv(d) for _, _, d in cases], bits, gs)
+    assert ex.perm13 is not None and ex.perm2 is not None
+    x = synth.activations(m, H, torch.float16, seed=m + 3)
+    idx, w = _routing(m, k, E, seed=m + 7)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex).float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("m", [1, 9, 70])
+def test_moe_router_weight_on_input(dev, m):
+    """apply_router_weight_on_input (top-1): the experts run on x * w (rounded), outputs unweighted."""
+    E, H, I, bits, gs = 4, 256, 128, 4, 128
+    cases, ref = _build(E, H, I, bits, gs, False, "fp16", seed=77 + m)
+    ex = _prepare(cases, bits, gs, dev)
+    x = synth.activations(m, H, torch.float16, seed=m)
+    idx, w = _routing(m, 1, E, seed=m + 1)
+    y = moe.moe_forward(x.to(dev), idx.to(dev), w.to(dev), ex, router_weight_on_input=True).float().cpu().numpy()
+    xs = (x * w.to(torch.float16)).float().numpy()  # fp16 product, as vLLM scales the hidden states
+    want = om.moe_forward(xs, idx.numpy(), np.ones((m, 1), np.float32), ref, "silu")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err
+    with pytest.raises(ValueError):
+        idx2, w2 = _routing(m, 2, E, seed=m + 2)
+        moe.moe_forward(x.to(dev), idx2.to(dev), w2.to(dev), ex, router_weight_on_input=True)
+
+
+def test_vllm_fused_moe_layer_act_order(dev):
+    """desc_act: w13_g_idx / w2_g_idx registered and loaded per shard (gate and up into one row)."""
+    from onecompression_amd import gptq as G
+    from onecompression_amd.vllm_compat import HAS_VLLM, FusedMoE
+
+    if HAS_VLLM:
+        pytest.skip("uses the stand-in FusedMoE")
+    E, H, I, k, gs, m, bits = 4, 256, 128, 2, 128, 6, 4
+    qb = [{f"mlp.experts.{e}.{p}": {"bits": bits, "method": "gptq", "group_size": gs}
+           for e in range(E) for p in ("gate_proj", "up_proj", "down_proj")}]
+    cfg = G.MixedGPTQConfig(quantization_bits=qb, group_size=-1, desc_act=True, sym=False, checkpoint_format="gptq")
+    layer = FusedMoE(E, k, H, I, quant_config=cfg, prefix="model.layers.0.mlp.experts", activation="silu")
+    assert tuple(layer.w13_g_idx.shape) == (E, H) and tuple(layer.w2_g_idx.shape) == (E, I)
+    cases, ref = _build_act_order(E, H, I, bits, gs, "fp16", seed=910)
+    for e, (g, u, d) in enumerate(cases):
+        for sid, c in (("w1", g), ("w3", u), ("w2", d)):
+            pre = "w2" if sid == "w2" else "w13"
+            for t in ("qweight", "qzeros", "scales", "g_idx"):
+                layer.weight_loader(getattr(layer, f"{pre}_{t}"), getattr(c, t), f"experts.{pre}_{t}", sid, e)
+    layer.to(dev)
+    layer.quant_method.process_weights_after_loading(layer)
+    x = synth.activations(m, H, torch.float16, seed=27)
+    idx, w = _routing(m, k, E, seed=28)
+    y = layer(x.to(dev), w.to(dev), idx.to(dev)).float().cpu().numpy()
+    want = om.moe_forward(x.float().numpy(), idx.numpy(), w.numpy(), ref, "silu")
+    err = float(np.max(np.abs(y - want)) / np.max(np.abs(want)))
+    assert err <= 1e-2, err

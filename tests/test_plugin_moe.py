@@ -98,10 +98,40 @@ def test_loader_places_gate_up_down_and_bias():
     assert layer.weight_loader(layer.w2_bias, torch.zeros(H), "experts.w2_bias", "w2", 1, return_success=True)
 
 
-def test_apply_before_processing_and_unsupported_options():
+def test_apply_before_processing():
     layer = _moe(0)
     x = torch.zeros(1, 128, dtype=torch.float16)
     with pytest.raises(RuntimeError):
         layer(x, torch.ones(1, 2), torch.zeros(1, 2, dtype=torch.int32))
-    with pytest.raises(NotImplementedError):
-        G.GPTQMoEMethod(G.GPTQLayerConfig(4, 128, True, False, "gptq"))
+
+
+def test_act_order_g_idx_params_and_loader():
+    """desc_act registers w13_g_idx [E, H] (gate and up share a row, which must agree) and
+    w2_g_idx [E, I]."""
+    from onecompression_amd.vllm_compat import FusedMoE
+
+    cfg = G.MixedGPTQConfig(quantization_bits=QB, group_size=128, desc_act=True, sym=False, checkpoint_format="gptq")
+    E, H, I = 4, 128, 64
+    layer = FusedMoE(E, 2, H, I, quant_config=cfg, prefix="model.layers.0.mlp.experts")
+    assert tuple(layer.w13_g_idx.shape) == (E, H) and layer.w13_g_idx.dtype == torch.int32
+    assert tuple(layer.w2_g_idx.shape) == (E, I)
+    g = synth.gptq_case("g", H, I, 3, 64, True, seed=1).g_idx
+    layer.weight_loader(layer.w13_g_idx, g, "experts.w13_g_idx", "w1", 2)
+    layer.weight_loader(layer.w13_g_idx, g, "experts.w13_g_idx", "w3", 2)  # same order: accepted
+    assert torch.equal(layer.w13_g_idx.data[2], g)
+    with pytest.raises(ValueError, match="g_idx differ"):
+        layer.weight_loader(layer.w13_g_idx, torch.flip(g, [0]), "experts.w13_g_idx", "w3", 2)
+    d = synth.gptq_case("d", I, H, 3, 64, True, seed=2).g_idx
+    layer.weight_loader(layer.w2_g_idx, d, "experts.w2_g_idx", "w2", 1)
+    assert torch.equal(layer.w2_g_idx.data[1], d)
+
+
+def test_prepare_experts_rejects_differing_gate_up_order():
+    from onecompression_amd import moe
+
+    g = synth.gptq_case("g", 128, 64, 4, 64, True, seed=3)
+    u = synth.gptq_case("u", 128, 64, 4, 64, True, seed=4)
+    d = synth.gptq_case("d", 64, 128, 4, 64, True, seed=5)
+    t = lambda c: (c.qweight, c.qzeros, c.scales, c.g_idx)  # noqa: E731
+    with pytest.raises(ValueError, match="same g_idx"):
+        moe.prepare_experts([t(g)], [t(u)], [t(d)], 4, 64)
