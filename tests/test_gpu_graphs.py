@@ -34,6 +34,8 @@ def _replays(dev, make_inputs, run, n=3):
     (4096, 28672, 3, 4, torch.float16),   # balanced streaming GEMV (wide, uneven CU load)
     (4096, 4096, 4, 1, torch.float16),    # k_gemv
     (1024, 16384, 2, 24, torch.float16),  # streaming GEMM (mid M)
+    (4096, 4096, 4, 128, torch.float16),  # streaming GEMM, 8 row blocks, K split + reduce
+    (14336, 4096, 2, 48, torch.bfloat16), # streaming GEMM, 4 row blocks, long K split
     (512, 1024, 8, 40, torch.bfloat16),   # skinny / split-K
     (1024, 1024, 4, 300, torch.bfloat16), # large-M GEMM
 ])
@@ -51,7 +53,7 @@ def test_gptq_grouped_graph(dev):
              lambda b: ops.gptq_gemm_grouped(b[0], preps))
 
 
-@pytest.mark.parametrize("m", [1, 64])
+@pytest.mark.parametrize("m", [1, 64, 200])
 def test_dbf_and_mdbf_graph(dev, m):
     c = synth.dbf_case("d", 1024, 2048, 1.0, seed=5).to(dev)
     part = dbf_ops.dbf_prepare(c.s0, c.bp1, c.s2, c.bp3, c.s4, c.in_features, c.mid, c.out_features)
@@ -63,6 +65,9 @@ def test_dbf_and_mdbf_graph(dev, m):
                                      torch.ones((c.mid, 1), dtype=torch.float16, device=dev))
     _replays(dev, lambda i: [synth.activations(m, 1024, torch.float16, seed=70 + i)],
              lambda b: dbf_ops.mdbf_forward(b[0], [path]))
+    # two paths: one sign GEMM over both terms' k-blocks above 16 rows
+    _replays(dev, lambda i: [synth.activations(m, 1024, torch.float16, seed=75 + i)],
+             lambda b: dbf_ops.mdbf_forward(b[0], [path, path]))
 
 
 @pytest.mark.parametrize("rounding", ["stages", "once", "fp32"])
