@@ -425,6 +425,250 @@ __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int 
   if (c < c1) out[(size_t)blockIdx.x * ld_out + c] = 0;
 }
 
+// ---------------------------------------------------------------------------
+// One term at 16 < M <= 64: one wave per 16-row output tile streams its
+// share of the term's k-blocks; the workgroup's 4 waves (4 consecutive tiles)
+// share x, staged one k-block (128 k) at a time in a two-buffer LDS ring with
+// the pre scale applied on the way (RNE(in * pre), the reference's rounding),
+// so no separate scaling launch and no 64-row padding.  Each +-1 B operand
+// decoded from a sign word feeds MB = ceil(M / 16) MFMAs.  The sign words run
+// D k-blocks ahead in registers, x two k-blocks ahead.  Rows too few to fill
+// the GPU split K over blockIdx.y: each split's fp32 sums (post-scaled) go to
+// partial[split][m][n] and k_sign_reduce adds them in split order.
+// The k-block barrier waits for LDS traffic only (no wait for the prefetches).
+// ---------------------------------------------------------------------------
+constexpr int kSignStreamMaxM = 64;
+
+struct SignStreamArgs {
+  const uint32_t* sg;     // sign layout of the term
+  const uint16_t* in;     // [M, ld_in]
+  const uint16_t* pre;    // [round8(Kd)] zero-padded, or null
+  const uint16_t* post;   // [R] or null (scale 1)
+  const uint16_t* bias;   // [R] or null (S == 1 only)
+  uint16_t* out;          // [M, ld_out]
+  float* partial;         // [S, M, N_pad] when S > 1
+  int ld_in, ld_out, M, Kd, R, RT, NU, uk_shift, NKB, kps, S, fill_to, N_pad;
+};
+
+template <int MB, bool PRE, bool BF16>
+__global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) {
+  constexpr int XLD = 136, ROWS = 16 * MB, D = 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, kq = lane >> 4;
+  const int rt = blockIdx.x * 4 + wave;
+  const int rtc = min(rt, a.RT - 1);  // waves past the last tile compute the last one, unused
+  const int split = blockIdx.y;
+  const int kb0 = split * a.kps, kb1 = min(kb0 + a.kps, a.NKB);
+  const int M = a.M;
+  const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
+  const uint32_t smask = oc_opaque(0x80008000u);
+
+  extern __shared__ __align__(16) uint16_t xl[];  // [2][ROWS][XLD]
+  // staging of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at 8 (c % 16));
+  // chunks at k >= Kd and rows >= M read zero (offsets past the descriptors)
+  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.in, (uint32_t)M * a.ld_in * 2);
+  const __amdgpu_buffer_rsrc_t pr = oc_rsrc(a.pre, (uint32_t)((a.Kd + 7) / 8 * 8) * 2);
+  const int ck = 8 * (threadIdx.x & 15);
+  oc_u4 xs_reg[MB], ps_reg;
+  auto stage_load = [&](int kb) {
+    const int k = kb * 128 + ck;
+    const bool kok = k < a.Kd;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int row = (threadIdx.x + 256 * j) >> 4;
+      xs_reg[j] = oc_bload16(xr, kok && row < M ? (uint32_t)(row * a.ld_in + k) * 2 : kOcOob);
+    }
+    if constexpr (PRE) ps_reg = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int row = (threadIdx.x + 256 * j) >> 4;
+      oc_u4 v = xs_reg[j];
+      if constexpr (PRE) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], ps_reg[h]);
+      }
+      *(oc_u4*)(xl + (buf * ROWS + row) * XLD + ck) = v;
+    }
+  };
+  // sign word of k-block kb for this lane (word (rt, unit, lane, kbl) of the layout)
+  const int UKm = (1 << a.uk_shift) - 1;
+  const __amdgpu_buffer_rsrc_t sr =
+      oc_rsrc(a.sg + ((size_t)rtc * a.NU * 64 << a.uk_shift), (uint32_t)(a.NU * 64 << a.uk_shift) * 4);
+  auto load_w = [&](int kb) {
+    const uint32_t off = (uint32_t)(((((kb >> a.uk_shift) * 64 + lane) << a.uk_shift) + (kb & UKm)) * 4);
+    return __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 2);
+  };
+
+  oc_f4 yacc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) yacc[i] = oc_f4{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int kb, uint32_t w) {
+    const int buf = (kb - kb0) & 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int P = 4 * s;
+      const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
+                             ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const oc_u4 av = *(const oc_u4*)(xl + (buf * ROWS + 16 * i + col) * XLD + 32 * s + 8 * kq);
+        yacc[i] = oc_mfma16<BF16>(av, bv, yacc[i]);
+      }
+    }
+    stage_store(buf ^ 1);                // x of kb + 1 (its buffer was last read at kb - 1)
+    stage_load(min(kb + 2, kb1 - 1));    // past the end: the last k-block again, unused
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // prologue: x of kb0 (to LDS) and kb0 + 1 (registers), D sign words
+  stage_load(kb0);
+  stage_store(0);
+  stage_load(min(kb0 + 1, kb1 - 1));
+  uint32_t wr[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) wr[d] = load_w(min(kb0 + d, kb1 - 1));
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  for (int i0 = kb0; i0 < kb1; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int kb = i0 + d;
+      if (kb < kb1) {
+        consume(kb, wr[d]);
+        wr[d] = load_w(min(kb + D, kb1 - 1));
+      }
+    }
+  }
+
+  const int n = rt * 16 + col;
+  if (rt >= a.RT || n >= a.fill_to) return;
+  float ps = 0.f;  // columns R .. fill_to: zeros
+  if (n < a.R) ps = a.post ? (BF16 ? oc_bf2f(a.post[n]) : oc_h2f(a.post[n])) : 1.f;
+  if (a.S > 1) {
+    float* pp = a.partial + (size_t)split * M * a.N_pad + n;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + 4 * kq + r;
+        if (m < M) pp[(size_t)m * a.N_pad] = yacc[i][r] * ps;
+      }
+    return;
+  }
+  const float b = (a.bias && n < a.R) ? (BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n])) : 0.f;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * i + 4 * kq + r;
+      if (m < M) a.out[(size_t)m * a.ld_out + n] = BF16 ? oc_f2bf(fmaf(yacc[i][r], ps, b)) : oc_f2h(fmaf(yacc[i][r], ps, b));
+    }
+}
+
+// out[m, n] = sum over splits (in split order) of partial[s, m, n] (+ bias[n] for n < R), n < ncols.
+template <bool BF16>
+__global__ void k_sign_reduce(const float* __restrict__ partial, int S, int M, int ncols, int N_pad, int R,
+                              const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int ld_out) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (n >= ncols) return;
+  float o = 0.f;
+  for (int s = 0; s < S; ++s) o += partial[((size_t)s * M + m) * N_pad + n];
+  if (bias && n < R) o += BF16 ? oc_bf2f(bias[n]) : oc_h2f(bias[n]);
+  out[(size_t)m * ld_out + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
+}
+
+struct SignStreamPlan {
+  bool use;
+  int mb, S, kps;
+  size_t bytes;
+};
+
+// The streaming sign kernel serves one term at 16 < M <= 64 (OC_SIGN_STREAM = 0
+// turns it off, 1 forces it for any M <= 64); K splits: enough workgroups for
+// one per CU, at most 8, at least 4 k-blocks each (OC_SIGN_STREAM_S forces S).
+SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, int R, bool has_bias,
+                                int fill_to) {
+  SignStreamPlan p = {};
+  const int e = oc::knob("OC_SIGN_STREAM", -1);
+  const SignLayout L = make_sign_layout(R, terms[0].Kd);
+  p.use = n_terms == 1 && e != 0 && M <= kSignStreamMaxM && (e == 1 || M > kSignGemvMaxM) &&
+          !(has_bias && fill_to > R) && fill_to <= L.RT * 16;
+  if (!p.use) return p;
+  p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const int nkb = L.NU * L.UK, wgs = (L.RT + 3) / 4;
+  const int es = oc::knob("OC_SIGN_STREAM_S", 0);
+  int S = es > 0 ? es : (oc_device_cus() + wgs - 1) / wgs;
+  if (es <= 0) {
+    if (S > 8) S = 8;
+    if (S > nkb / 4) S = nkb / 4;
+  }
+  if (S > nkb) S = nkb;
+  if (S < 1) S = 1;
+  p.kps = (nkb + S - 1) / S;
+  p.S = (nkb + p.kps - 1) / p.kps;
+  p.bytes = p.S > 1 ? align256((size_t)p.S * M * L.RT * 16 * 4) : 0;
+  return p;
+}
+
+template <bool BF16>
+int launch_sign_stream(const SignStreamArgs& a, int mb, bool pre, hipStream_t st) {
+  const dim3 grid((a.RT + 3) / 4, a.S), block(256);
+  const size_t lds = (size_t)2 * 16 * mb * 136 * 2;
+#define OC_SS(MB_)                                                                               \
+  if (mb == MB_) {                                                                               \
+    if (pre) hipLaunchKernelGGL((k_sign_stream<MB_, true, BF16>), grid, block, lds, st, a);     \
+    else hipLaunchKernelGGL((k_sign_stream<MB_, false, BF16>), grid, block, lds, st, a);        \
+    OC_HIP(hipGetLastError());                                                                   \
+    return 0;                                                                                    \
+  }
+  OC_SS(1) OC_SS(2) OC_SS(4)
+#undef OC_SS
+  return oc::set_error(OC_ERR_UNSUPPORTED, "no streaming sign kernel for %d row blocks", mb);
+}
+
+int sign_stream(const oc_sign_term& T, int M, int R, bool bf16, const void* bias, void* out, int ld_out,
+                int fill_to, const SignStreamPlan& p, void* workspace, size_t ws_bytes, hipStream_t st) {
+  OC_REQUIRE(ws_bytes >= p.bytes && (p.bytes == 0 || workspace), OC_ERR_WORKSPACE,
+             "workspace of %zu bytes is smaller than the %zu required", ws_bytes, p.bytes);
+  const SignLayout L = make_sign_layout(R, T.Kd);
+  SignStreamArgs a = {};
+  a.sg = (const uint32_t*)T.packed;
+  a.in = (const uint16_t*)T.in;
+  a.pre = (const uint16_t*)T.pre;
+  a.post = (const uint16_t*)T.post;
+  a.bias = p.S == 1 ? (const uint16_t*)bias : nullptr;
+  a.out = (uint16_t*)out;
+  a.partial = (float*)workspace;
+  a.ld_in = T.ld_in;
+  a.ld_out = ld_out;
+  a.M = M;
+  a.Kd = T.Kd;
+  a.R = R;
+  a.RT = L.RT;
+  a.NU = L.NU;
+  a.uk_shift = L.UK == 4 ? 2 : (L.UK == 2 ? 1 : 0);
+  a.NKB = L.NU * L.UK;
+  a.kps = p.kps;
+  a.S = p.S;
+  a.fill_to = fill_to;
+  a.N_pad = L.RT * 16;
+  const bool pre = T.pre != nullptr;
+  const int rc = bf16 ? launch_sign_stream<true>(a, p.mb, pre, st) : launch_sign_stream<false>(a, p.mb, pre, st);
+  if (rc || p.S == 1) return rc;
+  const dim3 g((fill_to + 255) / 256, M);
+  if (bf16)
+    hipLaunchKernelGGL(k_sign_reduce<true>, g, dim3(256), 0, st, a.partial, p.S, M, fill_to, a.N_pad, R,
+                       (const uint16_t*)bias, (uint16_t*)out, ld_out);
+  else
+    hipLaunchKernelGGL(k_sign_reduce<false>, g, dim3(256), 0, st, a.partial, p.S, M, fill_to, a.N_pad, R,
+                       (const uint16_t*)bias, (uint16_t*)out, ld_out);
+  OC_HIP(hipGetLastError());
+  return 0;
+}
+
 struct SignGemmPlan {
   oc_gemm::GemmPlan gp;  // tiling (MDBF: over the terms' concatenated k-blocks)
   int mt;                // tile height 64 mt
@@ -583,10 +827,15 @@ int sign_gemm_large(const oc_sign_term* terms, int n_terms, int M, int R, bool b
 }  // namespace
 
 extern "C" size_t oc_sign_workspace_bytes(const oc_sign_term* terms, int n_terms, int M, int R) {
-  if (!terms || n_terms < 1 || n_terms > kMaxTerms || M < sign_gemm_min_m() || R <= 0) return 0;
+  if (!terms || n_terms < 1 || n_terms > kMaxTerms || R <= 0) return 0;
   for (int i = 0; i < n_terms; ++i)
     if (terms[i].Kd <= 0) return 0;
-  return plan_sign_gemm(terms, n_terms, M, R).bytes;
+  // the stream plan's split count does not depend on bias / fill_to, but a call with both takes
+  // the GEMM path: enough for either
+  const SignStreamPlan sp = plan_sign_stream(terms, n_terms, M, R, false, R);
+  const size_t gemm = M >= sign_gemm_min_m() ? plan_sign_gemm(terms, n_terms, M, R).bytes : 0;
+  if (sp.use) return sp.bytes > gemm ? sp.bytes : gemm;
+  return gemm;
 }
 
 extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R, int act_dtype,
@@ -622,6 +871,12 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
     a.t[i].Kd = T.Kd;
     a.t[i].NU = L.NU;
     a.t[i].UK = L.UK;
+  }
+  {
+    const SignStreamPlan sp = plan_sign_stream(terms, n_terms, M, R, bias != nullptr, fill_to);
+    if (sp.use)
+      return sign_stream(terms[0], M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to, sp, workspace,
+                         ws_bytes, (hipStream_t)stream);
   }
   if (M >= sign_gemm_min_m())
     return sign_gemm_large(terms, n_terms, M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to,

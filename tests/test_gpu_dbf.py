@@ -174,12 +174,18 @@ def test_sign_gemm_fill_and_bias(dev, dtype, m):
     assert torch.all(o[:, fill_to:] == 7.0)
 
 
-# 16 < M <= 64 on the large-M GEMM core (64-row tiles, K split with fp32 partials and a fixup):
-# pre and post scales, bias, fill_to of the rank stage, a rank stage of one-k-block units, bf16,
-# and the two-term MDBF stage.
+# 16 < M <= 64 on the streaming sign kernel (x staged per k-block with the pre scale applied,
+# K split over workgroups with an ordered reduce) and, pinned, on the large-M GEMM core (64-row
+# tiles, K split with fp32 partials and a fixup): pre and post scales, bias, fill_to of the rank
+# stage, a rank stage of one-k-block units, bf16.
 @pytest.mark.parametrize("m", [17, 32, 48, 64])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-def test_dbf_mid_m(dev, m, dtype):
+@pytest.mark.parametrize("path", ["stream", "gemm", "stream_s1", "stream_s3"])
+def test_dbf_mid_m(dev, m, dtype, path, plan):
+    if path == "gemm":
+        plan("OC_SIGN_STREAM", 0)
+    elif path != "stream":
+        plan("OC_SIGN_STREAM_S", int(path[-1]))
     k, n = 1408, 720  # r = 476: rank stage 30 tiles x 11 k-blocks, output stage 45 tiles x 4 k-blocks
     r, bp1, bp3, s0, s2, s4 = _factors(k, n, 900 + m)
     td = torch.float16 if dtype == "fp16" else torch.bfloat16
@@ -253,3 +259,17 @@ def test_sign_gemm_terms_signed_scales(dev, m, dtype, n_terms, with_bias):
     assert r <= (2e-3 if dtype == "fp16" else 8e-3), r
     assert torch.all(o[:, R:fill_to] == 0)
     assert torch.all(o[:, fill_to:] == 7.0)
+
+
+# The streaming sign kernel forced below its threshold (one 16-row block) and at the config-3
+# shapes with their automatic split counts, against the oracle.
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_sign_stream_forced_small_m(dev, m, plan):
+    plan("OC_SIGN_STREAM", 1)
+    k, n = 1408, 720
+    r, bp1, bp3, s0, s2, s4 = _factors(k, n, 1900 + m)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).half()
+    prep = dbf_ops.dbf_prepare(_t(s0, dev), _t(bp1, dev), _t(s2, dev), _t(bp3, dev), _t(s4, dev), k, r, n)
+    y = dbf_ops.dbf_forward(x.to(dev), [prep]).float().cpu().numpy()
+    ref = od.dbf_forward(x.numpy(), s0, bp1, s2, bp3, s4, k, r, n)
+    assert _rel(y, ref) <= 2e-3, _rel(y, ref)
