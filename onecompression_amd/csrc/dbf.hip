@@ -122,9 +122,12 @@ __device__ __forceinline__ uint32_t mul2(uint32_t a, uint32_t b) {
 // One workgroup per 16-row output tile; its W waves split each term's units
 // (u = wave, wave + W, ...) and keep D units in flight: the sign words, the
 // M x 128 UK slice of the input rows (XCH 16-byte chunks per lane) and, with
-// PRE, the lane's pre-scale chunk.  Every load is unconditional (invalid
-// chunks read a valid address and are zeroed after arrival), so the loads of
-// the next D - 1 units stay in flight while one unit is consumed.  The input
+// PRE, the lane's pre-scale chunk.  Every load is issued on every path
+// (chunks past Kd or rows >= M read zero at offsets past the buffer
+// descriptors; past a wave's last unit that unit is loaded again), so the
+// loads of the next D - 1 units stay in flight while one unit is consumed:
+// a load issued under a condition would make the compiler wait for all of
+// them (s_waitcnt vmcnt(0)) before each LDS store.  The input
 // slice is multiplied by the pre scale (RNE to the activation dtype, as the
 // reference's `x * scaling0.to(x.dtype)`), bounced through a wave-private LDS
 // slot to form the A operand, and multiplied by the +-1 pairs decoded from
@@ -158,7 +161,10 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
     }
     return;
   }
-  uint16_t* xslot = (uint16_t*)smem + (size_t)wave * M * XW;
+  // The slot holds XR = 64 XCH / CPR rows (>= M): every lane's chunk has a
+  // place, so the stores are unconditional (rows >= M hold zeros, unread).
+  constexpr int XR = 64 * XCH / CPR;
+  uint16_t* xslot = (uint16_t*)smem + (size_t)wave * XR * XW;
   const uint16_t* arow = xslot + min(col, M - 1) * XW + 8 * kq;
   // chunk q of this lane: row xm[q], k offset (inside the unit) xk (the same
   // for every q because 64 is a multiple of CPR)
@@ -214,45 +220,58 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
       const bool kok = k < T.Kd;
 #pragma unroll
       for (int q = 0; q < XCH; ++q)
-        xb[q] = oc_bload16(xr, kok && xm[q] < M ? (uint32_t)(xm[q] * T.ld_in + k) * 2 : kOcOob);
+        xb[q] = oc_bload16(xr, (kok & (xm[q] < M)) ? (uint32_t)(xm[q] * T.ld_in + k) * 2 : kOcOob);
       if constexpr (PRE) pb[0] = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
     };
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d < n_my) load_unit(d, sbuf[d], xbuf[d], pbuf[d]);
 
     oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
-    for (int i0 = 0; i0 < n_my; i0 += D) {
+    if (n_my > 0) {
+      // Every load is issued on every path (past the wave's last unit: that
+      // unit again, unused), so the count of loads in flight is the same
+      // everywhere and each wait is for exactly the unit being consumed.
+      // (the scheduling barriers keep the units' loads in unit order: the
+      // wait counts at the loop head assume it)
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        const int i = i0 + d;
-        if (i >= n_my) break;
-        // Lanes read what other lanes of the same wave wrote: the compiler
-        // barriers order the exchange (a wave's DS operations run in order).
-        oc_wave_lds_barrier();
+        load_unit(min(d, n_my - 1), sbuf[d], xbuf[d], pbuf[d]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      for (int i0 = 0; i0 < n_my; i0 += D) {
 #pragma unroll
-        for (int q = 0; q < XCH; ++q) {
-          oc_u4 v = xbuf[d][q];
-          if constexpr (PRE) {
+        for (int d = 0; d < D; ++d) {
+          const int i = i0 + d;
+          if (i < n_my) {
+            // Lanes read what other lanes of the same wave wrote: the compiler
+            // barriers order the exchange (a wave's DS operations run in order).
+            oc_wave_lds_barrier();
 #pragma unroll
-            for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], pbuf[d][0][h]);
+            for (int q = 0; q < XCH; ++q) {
+              oc_u4 v = xbuf[d][q];
+              if constexpr (PRE) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], pbuf[d][0][h]);
+              }
+              *(oc_u4*)(xslot + xm[q] * XW + xk) = v;
+            }
+            oc_wave_lds_barrier();
+#pragma unroll
+            for (int kbl = 0; kbl < UK; ++kbl) {
+              oc_u4 av[4];
+#pragma unroll
+              for (int s = 0; s < 4; ++s) av[s] = *(const oc_u4*)(arow + kbl * 128 + 32 * s);
+              const uint32_t w = sbuf[d][kbl];
+#pragma unroll
+              for (int s = 0; s < 4; ++s) {
+                const int P = 4 * s;
+                const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
+                                       ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
+                acc = oc_mfma16<BF16>(av[s], bv, acc);
+              }
+            }
           }
-          if (xm[q] < M) *(oc_u4*)(xslot + xm[q] * XW + xk) = v;
+          load_unit(min(i + D, n_my - 1), sbuf[d], xbuf[d], pbuf[d]);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        oc_wave_lds_barrier();
-#pragma unroll
-        for (int kbl = 0; kbl < UK; ++kbl) {
-          const uint32_t w = sbuf[d][kbl];
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const oc_u4 av = *(const oc_u4*)(arow + kbl * 128 + 32 * s);
-            const int P = 4 * s;
-            const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
-                                   ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
-            acc = oc_mfma16<BF16>(av, bv, acc);
-          }
-        }
-        if (i + D < n_my) load_unit(i + D, sbuf[d], xbuf[d], pbuf[d]);
       }
     }
     uint16_t pr16 = praw[0];
@@ -287,18 +306,28 @@ constexpr size_t kSignLds = 64 * 1024;
 // Waves per workgroup (4, 8 or 16): enough waves in total to cover the GPU
 // (the rank-side stage has few row tiles), no more than the units allow, and
 // an LDS x slot per wave.
+// XCH = 16-byte input chunks per lane and unit (M * 16 UK chunks over 64
+// lanes, rounded up to a power of two); an x slot holds 4 XCH / UK rows.
+int sign_xch(int M, int UK) {
+  const int xc = (M * UK + 3) / 4;
+  int x = 1;
+  while (x < xc) x *= 2;
+  return x;
+}
+size_t sign_slot_bytes(int M, int UK) { return (size_t)(4 * sign_xch(M, UK) / UK) * (UK * 128 + 8) * 2; }
+
 int sign_waves(int RT, int NU, int M, int UK) {
   const int e = oc::knob("OC_SIGN_W", 0);
   int w = (e == 4 || e == 8 || e == 16) ? e : (RT >= 768 ? 4 : (RT >= 384 ? 8 : 16));
   while (w > 4 && w > NU) w /= 2;
-  const size_t slot = (size_t)M * (UK * 128 + 8) * 2;
+  const size_t slot = sign_slot_bytes(M, UK);
   while (w > 4 && slot * w > kSignLds) w /= 2;
   return w;
 }
 
 template <int UK, int XCH, bool BF16>
 int launch_sign_x(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
-  const size_t slot = (size_t)a.M * (UK * 128 + 8) * 2;
+  const size_t slot = (size_t)(4 * XCH / UK) * (UK * 128 + 8) * 2;
   const size_t xb = slot * a.W;
   const size_t rb = (size_t)a.W * 4 * 64 * 4;
   const size_t lds = ((xb > rb ? xb : rb) + 15) / 16 * 16;
@@ -314,10 +343,9 @@ int launch_sign_x(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
   return 0;
 }
 
-// XCH = 16-byte input chunks per lane and unit: M * 16 UK chunks over 64 lanes.
 template <int UK, bool BF16>
 int launch_sign(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
-  const int xc = (a.M * UK + 3) / 4;
+  const int xc = sign_xch(a.M, UK);
   if (xc <= 1) return launch_sign_x<UK, 1, BF16>(a, pre, rt_grid, st);
   if (xc <= 2) return launch_sign_x<UK, 2, BF16>(a, pre, rt_grid, st);
   if (xc <= 4) return launch_sign_x<UK, 4, BF16>(a, pre, rt_grid, st);
@@ -431,10 +459,17 @@ __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int 
 // share x, staged one k-block (128 k) at a time in a two-buffer LDS ring with
 // the pre scale applied on the way (RNE(in * pre), the reference's rounding),
 // so no separate scaling launch and no 64-row padding.  Each +-1 B operand
-// decoded from a sign word feeds MB = ceil(M / 16) MFMAs.  The sign words run
-// D k-blocks ahead in registers, x two k-blocks ahead.  Rows too few to fill
-// the GPU split K over blockIdx.y: each split's fp32 sums (post-scaled) go to
-// partial[split][m][n] and k_sign_reduce adds them in split order.
+// decoded from a sign word feeds MB = ceil(M / 16) MFMAs.
+// Latency: a wave's k-block step is a few hundred cycles and there are few
+// waves per SIMD, so the loads run far ahead in registers: the sign words
+// 12 k-blocks (whole units of UK words, one 4/8/16-byte load per lane), the
+// x and pre-scale chunks XL = 4 k-blocks (a register ring; the LDS store of
+// the next k-block waits only for a load issued XL steps earlier).  The loop
+// is unrolled over a period of 12 k-blocks so that every ring index is a
+// constant; a split's last partial period runs guarded.
+// Rows too few to fill the GPU split K (on unit boundaries) over blockIdx.y:
+// each split's fp32 sums (post-scaled) go to partial[split][m][n] and
+// k_sign_reduce adds them in split order.
 // The k-block barrier waits for LDS traffic only (no wait for the prefetches).
 // ---------------------------------------------------------------------------
 constexpr int kSignStreamMaxM = 64;
@@ -447,100 +482,123 @@ struct SignStreamArgs {
   const uint16_t* bias;   // [R] or null (S == 1 only)
   uint16_t* out;          // [M, ld_out]
   float* partial;         // [S, M, N_pad] when S > 1
-  int ld_in, ld_out, M, Kd, R, RT, NU, uk_shift, NKB, kps, S, fill_to, N_pad;
+  int ld_in, ld_out, M, Kd, R, RT, NU, ups, S, fill_to, N_pad;
 };
 
-template <int MB, bool PRE, bool BF16>
+template <int MB, int UK, bool PRE, bool BF16>
 __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) {
-  constexpr int XLD = 136, ROWS = 16 * MB, D = 4;
+  constexpr int XLD = 136, ROWS = 16 * MB;
+  constexpr int XL = 4;          // x k-blocks in flight
+  constexpr int DU = 12 / UK;    // sign units in flight
+  constexpr int PER = DU * UK;   // unroll period (k-blocks)
+  static_assert(PER % XL == 0 && PER % 2 == 0, "ring indices must repeat every period");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kq = lane >> 4;
   const int rt = blockIdx.x * 4 + wave;
   const int rtc = min(rt, a.RT - 1);  // waves past the last tile compute the last one, unused
   const int split = blockIdx.y;
-  const int kb0 = split * a.kps, kb1 = min(kb0 + a.kps, a.NKB);
+  const int u0 = split * a.ups, u1 = min(u0 + a.ups, a.NU);
+  const int kb0 = u0 * UK, kb1 = u1 * UK;
   const int M = a.M;
   const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
   const uint32_t smask = oc_opaque(0x80008000u);
 
   extern __shared__ __align__(16) uint16_t xl[];  // [2][ROWS][XLD]
-  // staging of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at 8 (c % 16));
-  // chunks at k >= Kd and rows >= M read zero (offsets past the descriptors)
+  // x of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at
+  // 8 (c % 16)); chunks at k >= Kd and rows >= M read zero (offsets past the
+  // descriptors)
   const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.in, (uint32_t)M * a.ld_in * 2);
   const __amdgpu_buffer_rsrc_t pr = oc_rsrc(a.pre, (uint32_t)((a.Kd + 7) / 8 * 8) * 2);
   const int ck = 8 * (threadIdx.x & 15);
-  oc_u4 xs_reg[MB], ps_reg;
-  auto stage_load = [&](int kb) {
+  oc_u4 xq[XL][MB], pq[XL];
+  auto x_load = [&](int kb, oc_u4 (&xs)[MB], oc_u4& ps) {
     const int k = kb * 128 + ck;
     const bool kok = k < a.Kd;
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int row = (threadIdx.x + 256 * j) >> 4;
-      xs_reg[j] = oc_bload16(xr, kok && row < M ? (uint32_t)(row * a.ld_in + k) * 2 : kOcOob);
+      xs[j] = oc_bload16(xr, (kok & (row < M)) ? (uint32_t)(row * a.ld_in + k) * 2 : kOcOob);
     }
-    if constexpr (PRE) ps_reg = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
+    if constexpr (PRE) ps = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
   };
-  auto stage_store = [&](int buf) {
+  auto x_store = [&](int buf, const oc_u4 (&xs)[MB], const oc_u4& ps) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int row = (threadIdx.x + 256 * j) >> 4;
-      oc_u4 v = xs_reg[j];
+      oc_u4 v = xs[j];
       if constexpr (PRE) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], ps_reg[h]);
+        for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], ps[h]);
       }
       *(oc_u4*)(xl + (buf * ROWS + row) * XLD + ck) = v;
     }
   };
-  // sign word of k-block kb for this lane (word (rt, unit, lane, kbl) of the layout)
-  const int UKm = (1 << a.uk_shift) - 1;
-  const __amdgpu_buffer_rsrc_t sr =
-      oc_rsrc(a.sg + ((size_t)rtc * a.NU * 64 << a.uk_shift), (uint32_t)(a.NU * 64 << a.uk_shift) * 4);
-  auto load_w = [&](int kb) {
-    const uint32_t off = (uint32_t)(((((kb >> a.uk_shift) * 64 + lane) << a.uk_shift) + (kb & UKm)) * 4);
-    return __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 2);
+  // sign words of unit u for this lane: words (rt, u, lane, 0 .. UK-1) of the layout
+  const __amdgpu_buffer_rsrc_t sr = oc_rsrc(a.sg + (size_t)rtc * a.NU * 64 * UK, (uint32_t)a.NU * 64 * UK * 4);
+  uint32_t sw[DU][UK];
+  auto s_load = [&](int u, uint32_t (&sb)[UK]) {
+    const uint32_t so = (uint32_t)(u * 64 + lane) * UK * 4;
+    if constexpr (UK == 4) {
+      const oc_u4 v = oc_bload16_nt(sr, so);
+      sb[0] = v[0]; sb[1] = v[1]; sb[2] = v[2]; sb[3] = v[3];
+    } else if constexpr (UK == 2) {
+      typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+      const u2v v = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(sr, so, 0, 2));
+      sb[0] = v[0]; sb[1] = v[1];
+    } else {
+      sb[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 2);
+    }
   };
 
   oc_f4 yacc[MB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) yacc[i] = oc_f4{0.f, 0.f, 0.f, 0.f};
-  auto consume = [&](int kb, uint32_t w) {
-    const int buf = (kb - kb0) & 1;
+  // step d of a period (d a constant after unrolling) consumes k-block kb
+  auto step = [&](int kb, int d) {
+    // all of the step's A fragments first (one LDS latency per step, not one per MFMA)
+    oc_u4 av[4][MB];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        av[s][i] = *(const oc_u4*)(xl + ((d & 1) * ROWS + 16 * i + col) * XLD + 32 * s + 8 * kq);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t w = sw[d / UK][d % UK];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int P = 4 * s;
       const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
                              ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
 #pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const oc_u4 av = *(const oc_u4*)(xl + (buf * ROWS + 16 * i + col) * XLD + 32 * s + 8 * kq);
-        yacc[i] = oc_mfma16<BF16>(av, bv, yacc[i]);
-      }
+      for (int i = 0; i < MB; ++i) yacc[i] = oc_mfma16<BF16>(av[s][i], bv, yacc[i]);
     }
-    stage_store(buf ^ 1);                // x of kb + 1 (its buffer was last read at kb - 1)
-    stage_load(min(kb + 2, kb1 - 1));    // past the end: the last k-block again, unused
+    // x of kb + 1 into the other buffer (last read at kb - 1), then its ring
+    // slot takes x of kb + 1 + XL (past the end: the last k-block again, unused)
+    const int nx = (d + 1) % XL;
+    x_store((d + 1) & 1, xq[nx], pq[nx]);
+    x_load(min(kb + 1 + XL, kb1 - 1), xq[nx], pq[nx]);
+    if (d % UK == UK - 1) s_load(min(kb / UK + DU, u1 - 1), sw[d / UK]);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
-  // prologue: x of kb0 (to LDS) and kb0 + 1 (registers), D sign words
-  stage_load(kb0);
-  stage_store(0);
-  stage_load(min(kb0 + 1, kb1 - 1));
-  uint32_t wr[D];
+  // prologue: x of kb0 to LDS, ring slots j hold x of kb0 + j (slot 0: kb0 + XL),
+  // sign units u0 .. u0 + DU - 1
+  x_load(kb0, xq[0], pq[0]);
+  x_store(0, xq[0], pq[0]);
 #pragma unroll
-  for (int d = 0; d < D; ++d) wr[d] = load_w(min(kb0 + d, kb1 - 1));
+  for (int j = 1; j <= XL; ++j) x_load(min(kb0 + j, kb1 - 1), xq[j % XL], pq[j % XL]);
+#pragma unroll
+  for (int d = 0; d < DU; ++d) s_load(min(u0 + d, u1 - 1), sw[d]);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  for (int i0 = kb0; i0 < kb1; i0 += D) {
+  int base = kb0;
+  for (; base + PER <= kb1; base += PER) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int kb = i0 + d;
-      if (kb < kb1) {
-        consume(kb, wr[d]);
-        wr[d] = load_w(min(kb + D, kb1 - 1));
-      }
-    }
+    for (int d = 0; d < PER; ++d) step(base + d, d);
   }
+#pragma unroll
+  for (int d = 0; d < PER - 1; ++d)
+    if (base + d < kb1) step(base + d, d);
 
   const int n = rt * 16 + col;
   if (rt >= a.RT || n >= a.fill_to) return;
@@ -582,13 +640,14 @@ __global__ void k_sign_reduce(const float* __restrict__ partial, int S, int M, i
 
 struct SignStreamPlan {
   bool use;
-  int mb, S, kps;
+  int mb, S, ups;
   size_t bytes;
 };
 
 // The streaming sign kernel serves one term at 16 < M <= 64 (OC_SIGN_STREAM = 0
-// turns it off, 1 forces it for any M <= 64); K splits: enough workgroups for
-// one per CU, at most 8, at least 4 k-blocks each (OC_SIGN_STREAM_S forces S).
+// turns it off, 1 forces it for any M <= 64); K splits on unit boundaries:
+// enough workgroups for one per CU, at most 8, at least 4 k-blocks each
+// (OC_SIGN_STREAM_S forces S).
 SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, int R, bool has_bias,
                                 int fill_to) {
   SignStreamPlan p = {};
@@ -605,28 +664,35 @@ SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, i
     if (S > 8) S = 8;
     if (S > nkb / 4) S = nkb / 4;
   }
-  if (S > nkb) S = nkb;
+  if (S > L.NU) S = L.NU;
   if (S < 1) S = 1;
-  p.kps = (nkb + S - 1) / S;
-  p.S = (nkb + p.kps - 1) / p.kps;
+  p.ups = (L.NU + S - 1) / S;
+  p.S = (L.NU + p.ups - 1) / p.ups;
   p.bytes = p.S > 1 ? align256((size_t)p.S * M * L.RT * 16 * 4) : 0;
   return p;
 }
 
-template <bool BF16>
-int launch_sign_stream(const SignStreamArgs& a, int mb, bool pre, hipStream_t st) {
+template <int UK, bool BF16>
+int launch_sign_stream_uk(const SignStreamArgs& a, int mb, bool pre, hipStream_t st) {
   const dim3 grid((a.RT + 3) / 4, a.S), block(256);
   const size_t lds = (size_t)2 * 16 * mb * 136 * 2;
 #define OC_SS(MB_)                                                                               \
   if (mb == MB_) {                                                                               \
-    if (pre) hipLaunchKernelGGL((k_sign_stream<MB_, true, BF16>), grid, block, lds, st, a);     \
-    else hipLaunchKernelGGL((k_sign_stream<MB_, false, BF16>), grid, block, lds, st, a);        \
+    if (pre) hipLaunchKernelGGL((k_sign_stream<MB_, UK, true, BF16>), grid, block, lds, st, a); \
+    else hipLaunchKernelGGL((k_sign_stream<MB_, UK, false, BF16>), grid, block, lds, st, a);    \
     OC_HIP(hipGetLastError());                                                                   \
     return 0;                                                                                    \
   }
   OC_SS(1) OC_SS(2) OC_SS(4)
 #undef OC_SS
   return oc::set_error(OC_ERR_UNSUPPORTED, "no streaming sign kernel for %d row blocks", mb);
+}
+
+template <bool BF16>
+int launch_sign_stream(const SignStreamArgs& a, int uk, int mb, bool pre, hipStream_t st) {
+  if (uk == 4) return launch_sign_stream_uk<4, BF16>(a, mb, pre, st);
+  if (uk == 2) return launch_sign_stream_uk<2, BF16>(a, mb, pre, st);
+  return launch_sign_stream_uk<1, BF16>(a, mb, pre, st);
 }
 
 int sign_stream(const oc_sign_term& T, int M, int R, bool bf16, const void* bias, void* out, int ld_out,
@@ -649,14 +715,13 @@ int sign_stream(const oc_sign_term& T, int M, int R, bool bf16, const void* bias
   a.R = R;
   a.RT = L.RT;
   a.NU = L.NU;
-  a.uk_shift = L.UK == 4 ? 2 : (L.UK == 2 ? 1 : 0);
-  a.NKB = L.NU * L.UK;
-  a.kps = p.kps;
+  a.ups = p.ups;
   a.S = p.S;
   a.fill_to = fill_to;
   a.N_pad = L.RT * 16;
   const bool pre = T.pre != nullptr;
-  const int rc = bf16 ? launch_sign_stream<true>(a, p.mb, pre, st) : launch_sign_stream<false>(a, p.mb, pre, st);
+  const int rc = bf16 ? launch_sign_stream<true>(a, L.UK, p.mb, pre, st)
+                : launch_sign_stream<false>(a, L.UK, p.mb, pre, st);
   if (rc || p.S == 1) return rc;
   const dim3 g((fill_to + 255) / 256, M);
   if (bf16)
