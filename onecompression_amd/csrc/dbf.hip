@@ -122,12 +122,9 @@ __device__ __forceinline__ uint32_t mul2(uint32_t a, uint32_t b) {
 // One workgroup per 16-row output tile; its W waves split each term's units
 // (u = wave, wave + W, ...) and keep D units in flight: the sign words, the
 // M x 128 UK slice of the input rows (XCH 16-byte chunks per lane) and, with
-// PRE, the lane's pre-scale chunk.  Every load is issued on every path
-// (chunks past Kd or rows >= M read zero at offsets past the buffer
-// descriptors; past a wave's last unit that unit is loaded again), so the
-// loads of the next D - 1 units stay in flight while one unit is consumed:
-// a load issued under a condition would make the compiler wait for all of
-// them (s_waitcnt vmcnt(0)) before each LDS store.  The input
+// PRE, the lane's pre-scale chunk.  Every load is unconditional (invalid
+// chunks read a valid address and are zeroed after arrival), so the loads of
+// the next D - 1 units stay in flight while one unit is consumed.  The input
 // slice is multiplied by the pre scale (RNE to the activation dtype, as the
 // reference's `x * scaling0.to(x.dtype)`), bounced through a wave-private LDS
 // slot to form the A operand, and multiplied by the +-1 pairs decoded from
@@ -161,10 +158,7 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
     }
     return;
   }
-  // The slot holds XR = 64 XCH / CPR rows (>= M): every lane's chunk has a
-  // place, so the stores are unconditional (rows >= M hold zeros, unread).
-  constexpr int XR = 64 * XCH / CPR;
-  uint16_t* xslot = (uint16_t*)smem + (size_t)wave * XR * XW;
+  uint16_t* xslot = (uint16_t*)smem + (size_t)wave * M * XW;
   const uint16_t* arow = xslot + min(col, M - 1) * XW + 8 * kq;
   // chunk q of this lane: row xm[q], k offset (inside the unit) xk (the same
   // for every q because 64 is a multiple of CPR)
@@ -220,58 +214,45 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
       const bool kok = k < T.Kd;
 #pragma unroll
       for (int q = 0; q < XCH; ++q)
-        xb[q] = oc_bload16(xr, (kok & (xm[q] < M)) ? (uint32_t)(xm[q] * T.ld_in + k) * 2 : kOcOob);
+        xb[q] = oc_bload16(xr, kok && xm[q] < M ? (uint32_t)(xm[q] * T.ld_in + k) * 2 : kOcOob);
       if constexpr (PRE) pb[0] = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
     };
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < n_my) load_unit(d, sbuf[d], xbuf[d], pbuf[d]);
 
     oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
-    if (n_my > 0) {
-      // Every load is issued on every path (past the wave's last unit: that
-      // unit again, unused), so the count of loads in flight is the same
-      // everywhere and each wait is for exactly the unit being consumed.
-      // (the scheduling barriers keep the units' loads in unit order: the
-      // wait counts at the loop head assume it)
+    for (int i0 = 0; i0 < n_my; i0 += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        load_unit(min(d, n_my - 1), sbuf[d], xbuf[d], pbuf[d]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      for (int i0 = 0; i0 < n_my; i0 += D) {
+        const int i = i0 + d;
+        if (i >= n_my) break;
+        // Lanes read what other lanes of the same wave wrote: the compiler
+        // barriers order the exchange (a wave's DS operations run in order).
+        oc_wave_lds_barrier();
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-          const int i = i0 + d;
-          if (i < n_my) {
-            // Lanes read what other lanes of the same wave wrote: the compiler
-            // barriers order the exchange (a wave's DS operations run in order).
-            oc_wave_lds_barrier();
+        for (int q = 0; q < XCH; ++q) {
+          oc_u4 v = xbuf[d][q];
+          if constexpr (PRE) {
 #pragma unroll
-            for (int q = 0; q < XCH; ++q) {
-              oc_u4 v = xbuf[d][q];
-              if constexpr (PRE) {
-#pragma unroll
-                for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], pbuf[d][0][h]);
-              }
-              *(oc_u4*)(xslot + xm[q] * XW + xk) = v;
-            }
-            oc_wave_lds_barrier();
-#pragma unroll
-            for (int kbl = 0; kbl < UK; ++kbl) {
-              oc_u4 av[4];
-#pragma unroll
-              for (int s = 0; s < 4; ++s) av[s] = *(const oc_u4*)(arow + kbl * 128 + 32 * s);
-              const uint32_t w = sbuf[d][kbl];
-#pragma unroll
-              for (int s = 0; s < 4; ++s) {
-                const int P = 4 * s;
-                const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
-                                       ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
-                acc = oc_mfma16<BF16>(av[s], bv, acc);
-              }
-            }
+            for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], pbuf[d][0][h]);
           }
-          load_unit(min(i + D, n_my - 1), sbuf[d], xbuf[d], pbuf[d]);
-          __builtin_amdgcn_sched_barrier(0);
+          if (xm[q] < M) *(oc_u4*)(xslot + xm[q] * XW + xk) = v;
         }
+        oc_wave_lds_barrier();
+#pragma unroll
+        for (int kbl = 0; kbl < UK; ++kbl) {
+          const uint32_t w = sbuf[d][kbl];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const oc_u4 av = *(const oc_u4*)(arow + kbl * 128 + 32 * s);
+            const int P = 4 * s;
+            const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
+                                   ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
+            acc = oc_mfma16<BF16>(av, bv, acc);
+          }
+        }
+        if (i + D < n_my) load_unit(i + D, sbuf[d], xbuf[d], pbuf[d]);
       }
     }
     uint16_t pr16 = praw[0];
@@ -306,28 +287,18 @@ constexpr size_t kSignLds = 64 * 1024;
 // Waves per workgroup (4, 8 or 16): enough waves in total to cover the GPU
 // (the rank-side stage has few row tiles), no more than the units allow, and
 // an LDS x slot per wave.
-// XCH = 16-byte input chunks per lane and unit (M * 16 UK chunks over 64
-// lanes, rounded up to a power of two); an x slot holds 4 XCH / UK rows.
-int sign_xch(int M, int UK) {
-  const int xc = (M * UK + 3) / 4;
-  int x = 1;
-  while (x < xc) x *= 2;
-  return x;
-}
-size_t sign_slot_bytes(int M, int UK) { return (size_t)(4 * sign_xch(M, UK) / UK) * (UK * 128 + 8) * 2; }
-
 int sign_waves(int RT, int NU, int M, int UK) {
   const int e = oc::knob("OC_SIGN_W", 0);
   int w = (e == 4 || e == 8 || e == 16) ? e : (RT >= 768 ? 4 : (RT >= 384 ? 8 : 16));
   while (w > 4 && w > NU) w /= 2;
-  const size_t slot = sign_slot_bytes(M, UK);
+  const size_t slot = (size_t)M * (UK * 128 + 8) * 2;
   while (w > 4 && slot * w > kSignLds) w /= 2;
   return w;
 }
 
 template <int UK, int XCH, bool BF16>
 int launch_sign_x(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
-  const size_t slot = (size_t)(4 * XCH / UK) * (UK * 128 + 8) * 2;
+  const size_t slot = (size_t)a.M * (UK * 128 + 8) * 2;
   const size_t xb = slot * a.W;
   const size_t rb = (size_t)a.W * 4 * 64 * 4;
   const size_t lds = ((xb > rb ? xb : rb) + 15) / 16 * 16;
@@ -343,9 +314,10 @@ int launch_sign_x(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
   return 0;
 }
 
+// XCH = 16-byte input chunks per lane and unit: M * 16 UK chunks over 64 lanes.
 template <int UK, bool BF16>
 int launch_sign(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
-  const int xc = sign_xch(a.M, UK);
+  const int xc = (a.M * UK + 3) / 4;
   if (xc <= 1) return launch_sign_x<UK, 1, BF16>(a, pre, rt_grid, st);
   if (xc <= 2) return launch_sign_x<UK, 2, BF16>(a, pre, rt_grid, st);
   if (xc <= 4) return launch_sign_x<UK, 4, BF16>(a, pre, rt_grid, st);
@@ -514,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   oc_u4 xq[XL][MB], pq[XL];
   auto x_load = [&](int kb, oc_u4 (&xs)[MB], oc_u4& ps) {
     const int k = kb * 128 + ck;
-    const bool kok = k < a.Kd;
+    const bool kok = (k < a.Kd) & (kb < kb1);  // past the split's end: zero, no memory access
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int row = (threadIdx.x + 256 * j) >> 4;
@@ -538,7 +510,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   const __amdgpu_buffer_rsrc_t sr = oc_rsrc(a.sg + (size_t)rtc * a.NU * 64 * UK, (uint32_t)a.NU * 64 * UK * 4);
   uint32_t sw[DU][UK];
   auto s_load = [&](int u, uint32_t (&sb)[UK]) {
-    const uint32_t so = (uint32_t)(u * 64 + lane) * UK * 4;
+    const uint32_t so = u < u1 ? (uint32_t)(u * 64 + lane) * UK * 4 : kOcOob;  // past the split: zero
     if constexpr (UK == 4) {
       const oc_u4 v = oc_bload16_nt(sr, so);
       sb[0] = v[0]; sb[1] = v[1]; sb[2] = v[2]; sb[3] = v[3];
@@ -574,11 +546,11 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
       for (int i = 0; i < MB; ++i) yacc[i] = oc_mfma16<BF16>(av[s][i], bv, yacc[i]);
     }
     // x of kb + 1 into the other buffer (last read at kb - 1), then its ring
-    // slot takes x of kb + 1 + XL (past the end: the last k-block again, unused)
+    // slot takes x of kb + 1 + XL (past the split: zeros, no memory access)
     const int nx = (d + 1) % XL;
     x_store((d + 1) & 1, xq[nx], pq[nx]);
-    x_load(min(kb + 1 + XL, kb1 - 1), xq[nx], pq[nx]);
-    if (d % UK == UK - 1) s_load(min(kb / UK + DU, u1 - 1), sw[d / UK]);
+    x_load(kb + 1 + XL, xq[nx], pq[nx]);
+    if (d % UK == UK - 1) s_load(kb / UK + DU, sw[d / UK]);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -587,9 +559,9 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   x_load(kb0, xq[0], pq[0]);
   x_store(0, xq[0], pq[0]);
 #pragma unroll
-  for (int j = 1; j <= XL; ++j) x_load(min(kb0 + j, kb1 - 1), xq[j % XL], pq[j % XL]);
+  for (int j = 1; j <= XL; ++j) x_load(kb0 + j, xq[j % XL], pq[j % XL]);
 #pragma unroll
-  for (int d = 0; d < DU; ++d) s_load(min(u0 + d, u1 - 1), sw[d]);
+  for (int d = 0; d < DU; ++d) s_load(u0 + d, sw[d]);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   int base = kb0;
   for (; base + PER <= kb1; base += PER) {
