@@ -618,8 +618,9 @@ struct SignStreamPlan {
 
 // The streaming sign kernel serves one term at 16 < M <= 64 (OC_SIGN_STREAM = 0
 // turns it off, 1 forces it for any M <= 64); K splits on unit boundaries:
-// enough workgroups for one per CU, at most 8, at least 4 k-blocks each
-// (OC_SIGN_STREAM_S forces S).
+// enough workgroups for one per CU, at most 8, at least 4 k-blocks each, none
+// when the column workgroups alone cover 3/4 of the CUs (OC_SIGN_STREAM_S
+// forces S).
 SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, int R, bool has_bias,
                                 int fill_to) {
   SignStreamPlan p = {};
@@ -635,6 +636,9 @@ SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, i
   if (es <= 0) {
     if (S > 8) S = 8;
     if (S > nkb / 4) S = nkb / 4;
+    // column workgroups that already cover 3/4 of the CUs: no split, no
+    // reduce launch (up_proj's output stage at M = 32: 23.8 -> 21.5 us)
+    if (4 * wgs >= 3 * oc_device_cus()) S = 1;
   }
   if (S > L.NU) S = L.NU;
   if (S < 1) S = 1;

@@ -1130,7 +1130,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int c = threadIdx.x + 256 * j, row = c >> 4, k = kb * 128 + 8 * (c & 15);
-      xs_reg[j] = oc_bload16(xr, row < M && k < a.K ? (uint32_t)(row * a.K + k) * 2 : kOcOob);
+      // (& not &&: a short-circuit here can become branches around duplicated loads)
+      xs_reg[j] = oc_bload16(xr, ((row < M) & (k < a.K)) ? (uint32_t)(row * a.K + k) * 2 : kOcOob);
     }
   };
   auto stage_store = [&](int buf) {
@@ -1193,12 +1194,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
       if constexpr (SUMS) {
         const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
         const float oz = OFF + (float)(md >> 16);
+        oc_u4 av[MB][4];  // the k-block's A fragments first: one LDS latency, not one per MFMA
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) av[i][t] = *(const oc_u4*)(xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq + 32 * t);
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
-          const uint16_t* arow = xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq;
           oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(*(const oc_u4*)(arow + 32 * t), bq[t], acc);
+          for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(av[i][t], bq[t], acc);
           const oc_f4 xsv = *(const oc_f4*)(xsum + buf * ROWS + 16 * i + 4 * kq);
 #pragma unroll
           for (int r = 0; r < 4; ++r) yacc[i][r] = fmaf(sc, fmaf(-oz, xsv[r], acc[r]), yacc[i][r]);
@@ -1209,9 +1214,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
         for (int t = 0; t < 4; ++t) bq[t] = oc_gemm::gemm_apply<BF16>(bq[t], dq);
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
-          const uint16_t* arow = xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq;
+          oc_u4 av[4];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) yacc[i] = oc_mfma16<BF16>(*(const oc_u4*)(arow + 32 * t), bq[t], yacc[i]);
+          for (int t = 0; t < 4; ++t) av[t] = *(const oc_u4*)(xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq + 32 * t);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) yacc[i] = oc_mfma16<BF16>(av[t], bq[t], yacc[i]);
         }
       }
       stage_store(buf ^ 1);                  // k-block kb + 1 (its buffer was last read at kb - 1)
