@@ -1100,8 +1100,9 @@ __global__ __launch_bounds__(64 * kStreamBalWaves) void k_gemv_stream_bal(const 
 // for every outstanding global load, i.e. for the x and weight prefetches,
 // which would expose a memory round trip per k-block.
 // ---------------------------------------------------------------------------
-template <int BITS, int MB, bool BF16>
+template <int BITS, int MB, bool BF16, int NTW = 1>
 __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
+  static_assert(NTW == 1 || MB > 2, "two n-tiles per wave on the dequantised-B path only");
   using GG = Geo<BITS>;
   constexpr int U = GG::U, P = GG::P;
   constexpr int D = 2;        // units in flight per wave
@@ -1113,8 +1114,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kq = lane >> 4;
   const uint32_t msk = oc_opaque(GG::MASK), mag = oc_opaque(dec_magic<SUMS && BF16>());
-  const int nt = blockIdx.x * 4 + wave;
-  const int ntc = min(nt, a.NT_total - 1);  // waves past the last n-tile compute it, unused
+  // the wave's NTW n-tiles (NTW = 2: every A fragment read from LDS feeds two MFMAs, and
+  // a workgroup's x staging serves 32 NTW columns per wave)
+  const int nt0 = (blockIdx.x * 4 + wave) * NTW;
+  int ntc[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) ntc[j] = min(nt0 + j, a.NT_total - 1);  // past the last n-tile: computed, unused
   const int M = a.M;
   // this split's units (a multiple of D: the planner keeps NU / S even)
   const int split = blockIdx.y;
@@ -1155,43 +1160,59 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
   };
 
   const bool has_bias = a.bias != nullptr && a.S == 1;
-  const uint16_t braw = __builtin_amdgcn_raw_buffer_load_b16(
-      oc_rsrc(a.bias, (uint32_t)a.N * 2), has_bias && nt * 16 + col < a.N ? (uint32_t)(nt * 16 + col) * 2 : kOcOob,
-      0, 0);
-  const __amdgpu_buffer_rsrc_t wr = oc_rsrc(a.w + (size_t)ntc * a.NU * P * 1024, (uint32_t)a.NU * P * 1024);
+  uint16_t braw[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int n = (nt0 + j) * 16 + col;
+    braw[j] = __builtin_amdgcn_raw_buffer_load_b16(oc_rsrc(a.bias, (uint32_t)a.N * 2),
+                                                   has_bias && n < a.N ? (uint32_t)n * 2 : kOcOob, 0, 0);
+  }
+  __amdgpu_buffer_rsrc_t wr[NTW];
+  uint32_t mcol[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    wr[j] = oc_rsrc(a.w + (size_t)ntc[j] * a.NU * P * 1024, (uint32_t)a.NU * P * 1024);
+    mcol[j] = (uint32_t)(ntc[j] * 16 + col) * 4;
+  }
   const __amdgpu_buffer_rsrc_t mr = oc_rsrc(a.meta, (uint32_t)a.G * a.N_pad * 4);
-  const uint32_t mcol = (uint32_t)(ntc * 16 + col) * 4;
-  uint32_t wb[D][4 * P];
-  uint32_t mb[D][U];
-  auto load = [&](int u, uint32_t (&w)[4 * P], uint32_t (&m)[U]) {
+  uint32_t wb[D][NTW][4 * P];
+  uint32_t mb[D][NTW][U];
+  auto load = [&](int u, uint32_t (&w)[NTW][4 * P], uint32_t (&m)[NTW][U]) {
 #pragma unroll
-    for (int pt = 0; pt < P; ++pt) {
-      const oc_u4 v = oc_bload16_nt(wr, (uint32_t)(u * P + pt) * 1024 + lane * 16);
-      w[4 * pt] = v[0];
-      w[4 * pt + 1] = v[1];
-      w[4 * pt + 2] = v[2];
-      w[4 * pt + 3] = v[3];
-    }
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
-    for (int kbl = 0; kbl < U; ++kbl) {
-      const int g = (u * U + kbl) >> a.gkb_shift;
-      m[kbl] = __builtin_amdgcn_raw_buffer_load_b32(mr, mcol + (uint32_t)(g * a.N_pad) * 4, 0, 0);
-    }
+      for (int pt = 0; pt < P; ++pt) {
+        const oc_u4 v = oc_bload16_nt(wr[j], (uint32_t)(u * P + pt) * 1024 + lane * 16);
+        w[j][4 * pt] = v[0];
+        w[j][4 * pt + 1] = v[1];
+        w[j][4 * pt + 2] = v[2];
+        w[j][4 * pt + 3] = v[3];
+      }
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+      for (int kbl = 0; kbl < U; ++kbl) {
+        const int g = (u * U + kbl) >> a.gkb_shift;
+        m[j][kbl] = __builtin_amdgcn_raw_buffer_load_b32(mr, mcol[j] + (uint32_t)(g * a.N_pad) * 4, 0, 0);
+      }
   };
-  oc_f4 yacc[MB];
+  oc_f4 yacc[MB][NTW];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) yacc[i] = oc_f4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) yacc[i][j] = oc_f4{0.f, 0.f, 0.f, 0.f};
   const int kb_end = (ub + nu) * U;  // one past this split's last k-block
   // k-block kb: x from buffer (kb - first) & 1; afterwards the staged
   // registers of kb + 1 go to the other buffer, kb + 2 is loaded, one barrier.
-  auto consume = [&](int u, const uint32_t (&w)[4 * P], const uint32_t (&m)[U]) {
+  auto consume = [&](int u, const uint32_t (&w)[NTW][4 * P], const uint32_t (&m)[NTW][U]) {
 #pragma unroll
     for (int kbl = 0; kbl < U; ++kbl) {
       const int kb = u * U + kbl, buf = (kb - ub * U) & 1;
-      oc_u4 bq[4];
-      decode_kblock<BITS, SUMS && BF16>(w, kbl, bq, msk, mag);
-      const uint32_t md = m[kbl];
+      oc_u4 bq[NTW][4];
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) decode_kblock<BITS, SUMS && BF16>(w[j], kbl, bq[j], msk, mag);
       if constexpr (SUMS) {
+        const uint32_t md = m[0][kbl];
         const float sc = oc_h2f((uint16_t)(md & 0xFFFFu));
         const float oz = OFF + (float)(md >> 16);
         oc_u4 av[MB][4];  // the k-block's A fragments first: one LDS latency, not one per MFMA
@@ -1203,22 +1224,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
         for (int i = 0; i < MB; ++i) {
           oc_f4 acc = oc_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(av[i][t], bq[t], acc);
+          for (int t = 0; t < 4; ++t) acc = oc_mfma16<BF16>(av[i][t], bq[0][t], acc);
           const oc_f4 xsv = *(const oc_f4*)(xsum + buf * ROWS + 16 * i + 4 * kq);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) yacc[i][r] = fmaf(sc, fmaf(-oz, xsv[r], acc[r]), yacc[i][r]);
+          for (int r = 0; r < 4; ++r) yacc[i][0][r] = fmaf(sc, fmaf(-oz, xsv[r], acc[r]), yacc[i][0][r]);
         }
       } else {
-        const oc_gemm::GemmDeq<BF16> dq = oc_gemm::gemm_deq<BF16>(md);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) bq[t] = oc_gemm::gemm_apply<BF16>(bq[t], dq);
+        for (int j = 0; j < NTW; ++j) {
+          const oc_gemm::GemmDeq<BF16> dq = oc_gemm::gemm_deq<BF16>(m[j][kbl]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) bq[j][t] = oc_gemm::gemm_apply<BF16>(bq[j][t], dq);
+        }
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
           oc_u4 av[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) av[t] = *(const oc_u4*)(xl + (buf * ROWS + 16 * i + col) * XLD + 8 * kq + 32 * t);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) yacc[i] = oc_mfma16<BF16>(av[t], bq[t], yacc[i]);
+          for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) yacc[i][j] = oc_mfma16<BF16>(av[t], bq[j][t], yacc[i][j]);
         }
       }
       stage_store(buf ^ 1);                  // k-block kb + 1 (its buffer was last read at kb - 1)
@@ -1247,8 +1273,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
 #pragma unroll
   for (int d = 0; d < D; ++d) consume(ub + nu - D + d, wb[d], mb[d]);
 
-  const int n = nt * 16 + col;
-  if (nt < a.NT_total && n < a.N) {
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int n = (nt0 + j) * 16 + col;
+    if (nt0 + j >= a.NT_total || n >= a.N) continue;
     if (a.S > 1) {
       float* pp = a.partial + (size_t)split * M * a.N_pad + n;
 #pragma unroll
@@ -1256,17 +1284,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = 16 * i + 4 * kq + r;
-          if (m < M) pp[(size_t)m * a.N_pad] = yacc[i][r];
+          if (m < M) pp[(size_t)m * a.N_pad] = yacc[i][j][r];
         }
-      return;
+      continue;
     }
-    const float b = has_bias ? (BF16 ? oc_bf2f(braw) : oc_h2f(braw)) : 0.f;
+    const float b = has_bias ? (BF16 ? oc_bf2f(braw[j]) : oc_h2f(braw[j])) : 0.f;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 16 * i + 4 * kq + r;
-        if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(yacc[i][r] + b) : oc_f2h(yacc[i][r] + b);
+        if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(yacc[i][j][r] + b) : oc_f2h(yacc[i][j][r] + b);
       }
   }
 }
@@ -1488,9 +1516,9 @@ bool use_gemm_stream(const oc::Layout& L, int M, int gs) {
 // one per CU (two per CU on layers of >= 64 k-blocks), at most 8 splits, at
 // least 4 k-blocks per split, and an even number of units per split.
 // OC_GEMM_STREAM_S forces the count.
-int gemm_stream_split(const oc::Layout& L) {
+int gemm_stream_split(const oc::Layout& L, int ntw) {
   const int e = oc::knob("OC_GEMM_STREAM_S", 0);
-  const int wgs = (L.NT + 3) / 4, nkb = L.K_pad / 128;
+  const int wgs = (L.NT + 4 * ntw - 1) / (4 * ntw), nkb = L.K_pad / 128;
   const int target = oc_device_cus() * (nkb >= 64 ? 2 : 1);
   int S = e > 0 ? e : (target + wgs - 1) / wgs;
   if (e <= 0) {
@@ -1504,18 +1532,30 @@ int gemm_stream_split(const oc::Layout& L) {
 
 int gemm_stream_rows(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 64 ? 4 : 8)); }
 
+// n-tiles per wave of k_gemm_stream: 2 on the dequantised-B path (more than
+// 32 rows) of wide layers (>= 512 n-tiles: config-1 gate at M = 128 41.5 ->
+// 37.7 us, config-2 gate 42.8 -> 38.4); narrow layers keep 1 (half the
+// workgroups would need more K splits: config-1 o_proj at M = 128 19.6 ->
+// 21.6 us).  OC_GEMM_STREAM_NTW forces 1 or 2 on that path.
+int gemm_stream_ntw(const oc::Layout& L, int M) {
+  if (gemm_stream_rows(M) <= 2) return 1;
+  const int e = oc::knob("OC_GEMM_STREAM_NTW", 0);
+  if (e == 1 || e == 2) return e;
+  return L.NT >= 512 ? 2 : 1;
+}
+
 template <bool BF16>
 int dispatch_gemm_stream(int bits, int M, const oc::Layout& L, const StreamArgs& a, hipStream_t st) {
-  const int mbt = gemm_stream_rows(M);
-  const dim3 grid((L.NT + 3) / 4, a.S), block(256);
+  const int mbt = gemm_stream_rows(M), ntw = gemm_stream_ntw(L, M);
+  const dim3 grid((L.NT + 4 * ntw - 1) / (4 * ntw), a.S), block(256);
   const size_t lds = (size_t)2 * 16 * mbt * 136 * 2 + (mbt <= 2 ? (size_t)2 * 16 * mbt * 4 : 0);
-#define OC_GS(B_, MB_)                                                                      \
-  if (bits == B_ && mbt == MB_) {                                                           \
-    hipLaunchKernelGGL((k_gemm_stream<B_, MB_, BF16>), grid, block, lds, st, a);            \
+#define OC_GS(B_, MB_, NTW_)                                                                \
+  if (bits == B_ && mbt == MB_ && ntw == NTW_) {                                            \
+    hipLaunchKernelGGL((k_gemm_stream<B_, MB_, BF16, NTW_>), grid, block, lds, st, a);      \
     OC_HIP(hipGetLastError());                                                              \
     return 0;                                                                               \
   }
-#define OC_GSB(B_) OC_GS(B_, 1) OC_GS(B_, 2) OC_GS(B_, 4) OC_GS(B_, 8)
+#define OC_GSB(B_) OC_GS(B_, 1, 1) OC_GS(B_, 2, 1) OC_GS(B_, 4, 1) OC_GS(B_, 8, 1) OC_GS(B_, 4, 2) OC_GS(B_, 8, 2)
   OC_GSB(2) OC_GSB(3) OC_GSB(4) OC_GSB(8)
 #undef OC_GSB
 #undef OC_GS
@@ -1633,7 +1673,7 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
   const int gs = oc::eff_group(group_size, K);
   if (M <= kGemvMaxM && stream_depth(L, M, gs) > 0) return ws;
   if (use_gemm_stream(L, M, gs)) {
-    const int S = gemm_stream_split(L);
+    const int S = gemm_stream_split(L, gemm_stream_ntw(L, M));
     return S > 1 ? ws + align256((size_t)S * M * L.N_pad * 4) : ws;
   }
   if (M <= kGemvMaxM) {
@@ -1661,8 +1701,9 @@ extern "C" int oc_gptq_describe_plan(int M, int K, int N, int bits, int group_si
   const char* g = has_perm ? "k_gather + " : "";
   const int sd = M <= kGemvMaxM ? stream_depth(L, M, gs) : 0;
   if (sd == 0 && use_gemm_stream(L, M, gs)) {
-    const int S = gemm_stream_split(L);
-    snprintf(buf, len, "%sk_gemm_stream mb=%d S=%d%s", g, gemm_stream_rows(M), S, S > 1 ? " + k_splitk_reduce" : "");
+    const int S = gemm_stream_split(L, gemm_stream_ntw(L, M));
+    snprintf(buf, len, "%sk_gemm_stream mb=%d ntw=%d S=%d%s", g, gemm_stream_rows(M), gemm_stream_ntw(L, M), S,
+             S > 1 ? " + k_splitk_reduce" : "");
   } else if (M <= kGemvMaxM && sd > 0) {
     const int t = stream_bal_tiles(L, bits, M, stream_ksplit(L));
     if (t > 0) snprintf(buf, len, "%sk_gemv_stream_bal d=%d tiles_per_wg=%d", g, sd, t);
@@ -1731,7 +1772,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     a.gs = gs;
     a.gkb_shift = log2_exact(gs) - 7;
     a.ldy = ldy;
-    a.S = gemm_stream_split(L);
+    a.S = gemm_stream_split(L, gemm_stream_ntw(L, M));
     a.partial = (float*)ws;
     const int rc = bf16 ? dispatch_gemm_stream<true>(bits, M, L, a, st) : dispatch_gemm_stream<false>(bits, M, L, a, st);
     if (rc || a.S == 1) return rc;

@@ -367,13 +367,16 @@ def test_gemm_streaming_mid_m_variants(dev, bits, case, plan):
 # The streaming GEMM at 32 < M <= 128 (4 or 8 row blocks per B operand, dequantised B operand) and
 # its K split across workgroups (fp32 partials summed by k_splitk_reduce), forced by plan knobs:
 # splits the planner reduces to an even unit count, a ragged last n-tile, bias, bf16, act-order and
-# groups of 256.  Tolerances are regression bounds well under the 1e-2 contract.
+# groups of 256.  ntw = 2: two n-tiles per wave (45 or 46 n-tiles: the last wave's second n-tile
+# lies past the end).  Tolerances are regression bounds well under the 1e-2 contract.
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("m", [33, 64, 100, 128])
 @pytest.mark.parametrize("split", [1, 2, 4])
-def test_gemm_stream_mid_m_split(dev, bits, m, split, plan):
+@pytest.mark.parametrize("ntw", [1, 2])
+def test_gemm_stream_mid_m_split(dev, bits, m, split, ntw, plan):
     plan("OC_GEMM_STREAM", 1)
     plan("OC_GEMM_STREAM_S", split)
+    plan("OC_GEMM_STREAM_NTW", ntw)
     n = 720 if bits != 3 else 736
     _gemm_check(dev, _case(2048, n, bits, seed=400 + 7 * bits + m + split), m, "fp16", bias=(split == 2), tol=2e-3)
 
@@ -389,8 +392,10 @@ def test_gemm_tiled_mid_m(dev, bits, m, plan):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("case", ["bf16", "act", "g256", "wide"])
-def test_gemm_stream_mid_m_variants(dev, bits, case, plan):
+@pytest.mark.parametrize("ntw", [1, 2])
+def test_gemm_stream_mid_m_variants(dev, bits, case, ntw, plan):
     plan("OC_GEMM_STREAM", 1)
+    plan("OC_GEMM_STREAM_NTW", ntw)
     if case == "bf16":
         plan("OC_GEMM_STREAM_S", 2)
         _gemm_check(dev, _case(2048, 512, bits, seed=420 + bits), 96, "bf16", bias=True, tol=8e-3)
