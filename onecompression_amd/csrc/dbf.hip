@@ -457,13 +457,15 @@ struct SignStreamArgs {
   int ld_in, ld_out, M, Kd, R, RT, NU, ups, S, fill_to, N_pad;
 };
 
-template <int MB, int UK, bool PRE, bool BF16>
+template <int MB, int UK, int KPS, bool PRE, bool BF16>
 __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) {
-  constexpr int XLD = 136, ROWS = 16 * MB;
-  constexpr int XL = 4;          // x k-blocks in flight
-  constexpr int DU = 12 / UK;    // sign units in flight
-  constexpr int PER = DU * UK;   // unroll period (k-blocks)
-  static_assert(PER % XL == 0 && PER % 2 == 0, "ring indices must repeat every period");
+  constexpr int XLD = KPS * 128 + 8, ROWS = 16 * MB;
+  constexpr int XL = MB == 4 ? 2 : 4;  // x k-blocks in flight (2 at 64 rows: registers)
+  constexpr int DU = 12 / UK;     // sign units in flight
+  constexpr int PER = DU * UK;    // unroll period (k-blocks)
+  constexpr int CPP = PER / KPS;  // steps per period
+  static_assert(PER % XL == 0 && PER % KPS == 0 && CPP % 2 == 0 && XL % KPS == 0,
+                "ring indices must repeat every period");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kq = lane >> 4;
@@ -476,17 +478,17 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
   const uint32_t smask = oc_opaque(0x80008000u);
 
-  extern __shared__ __align__(16) uint16_t xl[];  // [2][ROWS][XLD]
+  extern __shared__ __align__(16) uint16_t xl[];  // [2][ROWS][XLD]: KPS k-blocks per buffer
   // x of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at
-  // 8 (c % 16)); chunks at k >= Kd and rows >= M read zero (offsets past the
-  // descriptors)
+  // 8 (c % 16)); chunks at k >= Kd, rows >= M and k-blocks past the split read
+  // zero (offsets past the descriptors, no memory access)
   const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.in, (uint32_t)M * a.ld_in * 2);
   const __amdgpu_buffer_rsrc_t pr = oc_rsrc(a.pre, (uint32_t)((a.Kd + 7) / 8 * 8) * 2);
   const int ck = 8 * (threadIdx.x & 15);
-  oc_u4 xq[XL][MB], pq[XL];
+  oc_u4 xq[XL][MB], pq[XL];  // slot j % XL: x (and pre) of k-block j of the period
   auto x_load = [&](int kb, oc_u4 (&xs)[MB], oc_u4& ps) {
     const int k = kb * 128 + ck;
-    const bool kok = (k < a.Kd) & (kb < kb1);  // past the split's end: zero, no memory access
+    const bool kok = (k < a.Kd) & (kb < kb1);
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int row = (threadIdx.x + 256 * j) >> 4;
@@ -494,7 +496,8 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
     }
     if constexpr (PRE) ps = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
   };
-  auto x_store = [&](int buf, const oc_u4 (&xs)[MB], const oc_u4& ps) {
+  // k-block kk of a step's KPS into LDS buffer buf
+  auto x_store = [&](int buf, int kk, const oc_u4 (&xs)[MB], const oc_u4& ps) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int row = (threadIdx.x + 256 * j) >> 4;
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
 #pragma unroll
         for (int h = 0; h < 4; ++h) v[h] = mul2<BF16>(v[h], ps[h]);
       }
-      *(oc_u4*)(xl + (buf * ROWS + row) * XLD + ck) = v;
+      *(oc_u4*)(xl + (buf * ROWS + row) * XLD + kk * 128 + ck) = v;
     }
   };
   // sign words of unit u for this lane: words (rt, u, lane, 0 .. UK-1) of the layout
@@ -526,51 +529,68 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   oc_f4 yacc[MB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) yacc[i] = oc_f4{0.f, 0.f, 0.f, 0.f};
-  // step d of a period (d a constant after unrolling) consumes k-block kb
-  auto step = [&](int kb, int d) {
+  // step c of a period (a constant after unrolling) consumes k-blocks kb .. kb + KPS - 1 (the
+  // period's KPS c ..) from LDS buffer c & 1
+  auto step = [&](int kb, int c) {
     // all of the step's A fragments first (one LDS latency per step, not one per MFMA)
-    oc_u4 av[4][MB];
+    oc_u4 av[KPS][4][MB];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int kk = 0; kk < KPS; ++kk)
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
-        av[s][i] = *(const oc_u4*)(xl + ((d & 1) * ROWS + 16 * i + col) * XLD + 32 * s + 8 * kq);
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          av[kk][s][i] = *(const oc_u4*)(xl + ((c & 1) * ROWS + 16 * i + col) * XLD + kk * 128 + 32 * s + 8 * kq);
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t w = sw[d / UK][d % UK];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int P = 4 * s;
-      const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
-                             ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
+    for (int kk = 0; kk < KPS; ++kk) {
+      const int d = KPS * c + kk;
+      const uint32_t w = sw[d / UK][d % UK];
 #pragma unroll
-      for (int i = 0; i < MB; ++i) yacc[i] = oc_mfma16<BF16>(av[s][i], bv, yacc[i]);
+      for (int s = 0; s < 4; ++s) {
+        const int P = 4 * s;
+        const oc_u4 bv = oc_u4{((w << P) & smask) | one2, ((w << (P + 1)) & smask) | one2,
+                               ((w << (P + 2)) & smask) | one2, ((w << (P + 3)) & smask) | one2};
+#pragma unroll
+        for (int i = 0; i < MB; ++i) yacc[i] = oc_mfma16<BF16>(av[kk][s][i], bv, yacc[i]);
+      }
     }
-    // x of kb + 1 into the other buffer (last read at kb - 1), then its ring
-    // slot takes x of kb + 1 + XL (past the split: zeros, no memory access)
-    const int nx = (d + 1) % XL;
-    x_store((d + 1) & 1, xq[nx], pq[nx]);
-    x_load(kb + 1 + XL, xq[nx], pq[nx]);
-    if (d % UK == UK - 1) s_load(kb / UK + DU, sw[d / UK]);
+    // x of the next step's k-blocks into the other buffer (last read by the
+    // previous step), then their ring slots take the k-blocks XL later
+#pragma unroll
+    for (int kk = 0; kk < KPS; ++kk) {
+      const int nx = (KPS * (c + 1) + kk) % XL;
+      x_store((c + 1) & 1, kk, xq[nx], pq[nx]);
+      x_load(kb + KPS + kk + XL, xq[nx], pq[nx]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KPS; ++kk) {
+      const int d = KPS * c + kk;
+      if (d % UK == UK - 1) s_load((kb + kk) / UK + DU, sw[d / UK]);
+    }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
-  // prologue: x of kb0 to LDS, ring slots j hold x of kb0 + j (slot 0: kb0 + XL),
-  // sign units u0 .. u0 + DU - 1
-  x_load(kb0, xq[0], pq[0]);
-  x_store(0, xq[0], pq[0]);
+  // prologue: x of the first KPS k-blocks to LDS (through ring slots 0 .. KPS-1),
+  // then slot j % XL takes k-block KPS + j; sign units u0 .. u0 + DU - 1
 #pragma unroll
-  for (int j = 1; j <= XL; ++j) x_load(kb0 + j, xq[j % XL], pq[j % XL]);
+  for (int kk = 0; kk < KPS; ++kk) {
+    x_load(kb0 + kk, xq[kk], pq[kk]);
+    x_store(0, kk, xq[kk], pq[kk]);
+  }
+#pragma unroll
+  for (int j = KPS; j < KPS + XL; ++j) x_load(kb0 + j, xq[j % XL], pq[j % XL]);
 #pragma unroll
   for (int d = 0; d < DU; ++d) s_load(u0 + d, sw[d]);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   int base = kb0;
   for (; base + PER <= kb1; base += PER) {
 #pragma unroll
-    for (int d = 0; d < PER; ++d) step(base + d, d);
+    for (int c = 0; c < CPP; ++c) step(base + KPS * c, c);
   }
 #pragma unroll
-  for (int d = 0; d < PER - 1; ++d)
-    if (base + d < kb1) step(base + d, d);
+  for (int c = 0; c < CPP; ++c)
+    if (base + KPS * c < kb1) step(base + KPS * c, c);
 
   const int n = rt * 16 + col;
   if (rt >= a.RT || n >= a.fill_to) return;
@@ -648,16 +668,21 @@ SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, i
   return p;
 }
 
+// k-blocks per step (per barrier and LDS round trip): 2 up to 32 rows, 1 at 64
+// (the A fragments of two k-blocks of four row blocks would take 128 VGPRs)
+constexpr int sign_stream_kps(int mb) { return mb <= 2 ? 2 : 1; }
+
 template <int UK, bool BF16>
 int launch_sign_stream_uk(const SignStreamArgs& a, int mb, bool pre, hipStream_t st) {
   const dim3 grid((a.RT + 3) / 4, a.S), block(256);
-  const size_t lds = (size_t)2 * 16 * mb * 136 * 2;
-#define OC_SS(MB_)                                                                               \
-  if (mb == MB_) {                                                                               \
-    if (pre) hipLaunchKernelGGL((k_sign_stream<MB_, UK, true, BF16>), grid, block, lds, st, a); \
-    else hipLaunchKernelGGL((k_sign_stream<MB_, UK, false, BF16>), grid, block, lds, st, a);    \
-    OC_HIP(hipGetLastError());                                                                   \
-    return 0;                                                                                    \
+  const size_t lds = (size_t)2 * 16 * mb * (sign_stream_kps(mb) * 128 + 8) * 2;
+#define OC_SS(MB_)                                                                                         \
+  if (mb == MB_) {                                                                                         \
+    constexpr int KPS_ = sign_stream_kps(MB_);                                                             \
+    if (pre) hipLaunchKernelGGL((k_sign_stream<MB_, UK, KPS_, true, BF16>), grid, block, lds, st, a);     \
+    else hipLaunchKernelGGL((k_sign_stream<MB_, UK, KPS_, false, BF16>), grid, block, lds, st, a);        \
+    OC_HIP(hipGetLastError());                                                                             \
+    return 0;                                                                                              \
   }
   OC_SS(1) OC_SS(2) OC_SS(4)
 #undef OC_SS
