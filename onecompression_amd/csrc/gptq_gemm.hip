@@ -1512,9 +1512,10 @@ bool use_gemm_stream(const oc::Layout& L, int M, int gs) {
   return L.NT >= 1024 && (M > 12 || (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 64 > 80 * 1024);
 }
 
-// K splits of k_gemm_stream (workgroups of 4 n-tiles): enough workgroups for
-// one per CU (two per CU on layers of >= 64 k-blocks), at most 8 splits, at
-// least 4 k-blocks per split, and an even number of units per split.
+// K splits of k_gemm_stream (workgroups of 4 NTW n-tiles): enough workgroups
+// for one per CU (two per CU on layers of >= 64 k-blocks), at most 8 splits, at
+// least 4 k-blocks per split, none when the column workgroups cover 3/4 of the
+// CUs, and an even number of units per split.
 // OC_GEMM_STREAM_S forces the count.
 int gemm_stream_split(const oc::Layout& L, int ntw) {
   const int e = oc::knob("OC_GEMM_STREAM_S", 0);
@@ -1524,6 +1525,10 @@ int gemm_stream_split(const oc::Layout& L, int ntw) {
   if (e <= 0) {
     if (S > 8) S = 8;
     if (S > nkb / 4) S = nkb / 4;
+    // column workgroups alone cover 3/4 of the CUs: no split, no fp32 partials and no reduce
+    // (config-1 gate|up, 224 workgroups of two n-tiles per wave: M = 64 37.7 -> 29.8 us,
+    // M = 128 52.1 -> 46.2)
+    if (4 * wgs >= 3 * oc_device_cus()) S = 1;
   }
   if (S > L.NU / 2) S = L.NU / 2;
   while (S > 1 && (L.NU % (2 * S)) != 0) --S;
