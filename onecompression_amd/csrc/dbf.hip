@@ -426,36 +426,47 @@ __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int 
 }
 
 // ---------------------------------------------------------------------------
-// One term at 16 < M <= 64: one wave per 16-row output tile streams its
-// share of the term's k-blocks; the workgroup's 4 waves (4 consecutive tiles)
-// share x, staged one k-block (128 k) at a time in a two-buffer LDS ring with
-// the pre scale applied on the way (RNE(in * pre), the reference's rounding),
-// so no separate scaling launch and no 64-row padding.  Each +-1 B operand
-// decoded from a sign word feeds MB = ceil(M / 16) MFMAs.
-// Latency: a wave's k-block step is a few hundred cycles and there are few
-// waves per SIMD, so the loads run far ahead in registers: the sign words
-// 12 k-blocks (whole units of UK words, one 4/8/16-byte load per lane), the
-// x and pre-scale chunks XL = 4 k-blocks (a register ring; the LDS store of
-// the next k-block waits only for a load issued XL steps earlier).  The loop
-// is unrolled over a period of 12 k-blocks so that every ring index is a
-// constant; a split's last partial period runs guarded.
-// Rows too few to fill the GPU split K (on unit boundaries) over blockIdx.y:
-// each split's fp32 sums (post-scaled) go to partial[split][m][n] and
-// k_sign_reduce adds them in split order.
-// The k-block barrier waits for LDS traffic only (no wait for the prefetches).
+// 16 < M <= 64: one wave per 16-row output tile streams its share of a term's
+// k-blocks; the workgroup's 4 waves (4 consecutive tiles) share x, staged in a
+// two-buffer LDS ring (KPS = 2 k-blocks per buffer and barrier up to 32 rows,
+// 1 at 64) with the pre scale applied on the way (RNE(in * pre), the
+// reference's rounding), so no separate scaling launch and no 64-row padding.
+// Each +-1 B operand decoded from a sign word feeds MB = ceil(M / 16) MFMAs.
+// Latency: a wave's step is a few hundred cycles and there are few waves per
+// SIMD, so the loads run far ahead in registers: the sign words 12 k-blocks
+// (whole units of UK words, one 4/8/16-byte load per lane), the x and
+// pre-scale chunks XL = 4 k-blocks (2 at 64 rows; a register ring: the LDS
+// store of a k-block waits only for a load issued XL k-blocks earlier).  The
+// loop is unrolled over a period of 12 k-blocks so that every ring index is a
+// constant; a split's last partial period runs guarded.  The barrier waits
+// for LDS traffic only (no wait for the prefetches).
+// blockIdx.y = term * S + split: rows too few to fill the GPU split each
+// term's units S ways, and several terms (MDBF's paths) run side by side;
+// with T S > 1 each (term, split) writes its post-scaled fp32 sums to
+// partial[term S + split][m][n] and k_sign_reduce adds them in that order.
 // ---------------------------------------------------------------------------
 constexpr int kSignStreamMaxM = 64;
 
 struct SignStreamArgs {
-  const uint32_t* sg;     // sign layout of the term
-  const uint16_t* in;     // [M, ld_in]
-  const uint16_t* pre;    // [round8(Kd)] zero-padded, or null
-  const uint16_t* post;   // [R] or null (scale 1)
-  const uint16_t* bias;   // [R] or null (S == 1 only)
+  // per term (T of them): sign layout, input [M, ld_in], pre scale [round8(Kd)] zero-padded (all
+  // terms or none), post scale [R] or null (scale 1), Kd and units
+  const uint32_t* sg[kMaxTerms];
+  const uint16_t* in[kMaxTerms];
+  const uint16_t* pre[kMaxTerms];
+  const uint16_t* post[kMaxTerms];
+  int ld_in[kMaxTerms], Kd[kMaxTerms], NU[kMaxTerms];
+  const uint16_t* bias;   // [R] or null (T S == 1 only)
   uint16_t* out;          // [M, ld_out]
-  float* partial;         // [S, M, N_pad] when S > 1
-  int ld_in, ld_out, M, Kd, R, RT, NU, ups, S, fill_to, N_pad;
+  float* partial;         // [T S, M, N_pad] when T S > 1
+  int ld_out, M, R, RT, S, T, fill_to, N_pad;
 };
+
+// element t of a per-term argument array (t uniform; a compare chain, not a
+// dynamic index into the kernel arguments)
+template <class V>
+__device__ __forceinline__ V term_pick(int t, const V (&v)[kMaxTerms]) {
+  return t == 0 ? v[0] : (t == 1 ? v[1] : (t == 2 ? v[2] : v[3]));
+}
 
 template <int MB, int UK, int KPS, bool PRE, bool BF16>
 __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) {
@@ -471,8 +482,15 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   const int col = lane & 15, kq = lane >> 4;
   const int rt = blockIdx.x * 4 + wave;
   const int rtc = min(rt, a.RT - 1);  // waves past the last tile compute the last one, unused
-  const int split = blockIdx.y;
-  const int u0 = split * a.ups, u1 = min(u0 + a.ups, a.NU);
+  // blockIdx.y = term t * S + split: each term's units are cut into S splits
+  const int t = blockIdx.y / a.S, split = blockIdx.y - t * a.S;
+  const uint32_t* sg = term_pick(t, a.sg);
+  const uint16_t* in = term_pick(t, a.in);
+  const uint16_t* pre = term_pick(t, a.pre);
+  const uint16_t* post = term_pick(t, a.post);
+  const int ld_in = term_pick(t, a.ld_in), Kd = term_pick(t, a.Kd), NU = term_pick(t, a.NU);
+  const int ups = (NU + a.S - 1) / a.S;
+  const int u0 = split * ups, u1 = min(u0 + ups, NU);
   const int kb0 = u0 * UK, kb1 = u1 * UK;
   const int M = a.M;
   const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
@@ -482,17 +500,17 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   // x of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at
   // 8 (c % 16)); chunks at k >= Kd, rows >= M and k-blocks past the split read
   // zero (offsets past the descriptors, no memory access)
-  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.in, (uint32_t)M * a.ld_in * 2);
-  const __amdgpu_buffer_rsrc_t pr = oc_rsrc(a.pre, (uint32_t)((a.Kd + 7) / 8 * 8) * 2);
+  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(in, (uint32_t)M * ld_in * 2);
+  const __amdgpu_buffer_rsrc_t pr = oc_rsrc(pre, (uint32_t)((Kd + 7) / 8 * 8) * 2);
   const int ck = 8 * (threadIdx.x & 15);
   oc_u4 xq[XL][MB], pq[XL];  // slot j % XL: x (and pre) of k-block j of the period
   auto x_load = [&](int kb, oc_u4 (&xs)[MB], oc_u4& ps) {
     const int k = kb * 128 + ck;
-    const bool kok = (k < a.Kd) & (kb < kb1);
+    const bool kok = (k < Kd) & (kb < kb1);
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int row = (threadIdx.x + 256 * j) >> 4;
-      xs[j] = oc_bload16(xr, (kok & (row < M)) ? (uint32_t)(row * a.ld_in + k) * 2 : kOcOob);
+      xs[j] = oc_bload16(xr, (kok & (row < M)) ? (uint32_t)(row * ld_in + k) * 2 : kOcOob);
     }
     if constexpr (PRE) ps = oc_bload16(pr, kok ? (uint32_t)k * 2 : kOcOob);
   };
@@ -510,7 +528,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
     }
   };
   // sign words of unit u for this lane: words (rt, u, lane, 0 .. UK-1) of the layout
-  const __amdgpu_buffer_rsrc_t sr = oc_rsrc(a.sg + (size_t)rtc * a.NU * 64 * UK, (uint32_t)a.NU * 64 * UK * 4);
+  const __amdgpu_buffer_rsrc_t sr = oc_rsrc(sg + (size_t)rtc * NU * 64 * UK, (uint32_t)NU * 64 * UK * 4);
   uint32_t sw[DU][UK];
   auto s_load = [&](int u, uint32_t (&sb)[UK]) {
     const uint32_t so = u < u1 ? (uint32_t)(u * 64 + lane) * UK * 4 : kOcOob;  // past the split: zero
@@ -595,9 +613,9 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   const int n = rt * 16 + col;
   if (rt >= a.RT || n >= a.fill_to) return;
   float ps = 0.f;  // columns R .. fill_to: zeros
-  if (n < a.R) ps = a.post ? (BF16 ? oc_bf2f(a.post[n]) : oc_h2f(a.post[n])) : 1.f;
-  if (a.S > 1) {
-    float* pp = a.partial + (size_t)split * M * a.N_pad + n;
+  if (n < a.R) ps = post ? (BF16 ? oc_bf2f(post[n]) : oc_h2f(post[n])) : 1.f;
+  if (a.S * a.T > 1) {
+    float* pp = a.partial + (size_t)blockIdx.y * M * a.N_pad + n;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -632,39 +650,46 @@ __global__ void k_sign_reduce(const float* __restrict__ partial, int S, int M, i
 
 struct SignStreamPlan {
   bool use;
-  int mb, S, ups;
+  int mb, S, T;  // row blocks, K splits per term, terms (T S > 1: fp32 partials + k_sign_reduce)
   size_t bytes;
 };
 
-// The streaming sign kernel serves one term at 16 < M <= 64 (OC_SIGN_STREAM = 0
-// turns it off, 1 forces it for any M <= 64); K splits on unit boundaries:
-// enough workgroups for one per CU, at most 8, at least 4 k-blocks each, none
-// when the column workgroups alone cover 3/4 of the CUs (OC_SIGN_STREAM_S
-// forces S).
+// The streaming sign kernel serves 16 < M <= 64 (OC_SIGN_STREAM = 0 turns it
+// off, 1 forces it for any M <= 64), one term or up to four; K splits of each
+// term on unit boundaries: enough workgroups (all terms') for one per CU, at
+// most 8, at least 4 k-blocks each, none when the column workgroups alone cover
+// 3/4 of the CUs (OC_SIGN_STREAM_S forces S).
 SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, int R, bool has_bias,
                                 int fill_to) {
   SignStreamPlan p = {};
   const int e = oc::knob("OC_SIGN_STREAM", -1);
   const SignLayout L = make_sign_layout(R, terms[0].Kd);
-  p.use = n_terms == 1 && e != 0 && M <= kSignStreamMaxM && (e == 1 || M > kSignGemvMaxM) &&
-          !(has_bias && fill_to > R) && fill_to <= L.RT * 16;
+  p.use = n_terms >= 1 && n_terms <= kMaxTerms && e != 0 && M <= kSignStreamMaxM &&
+          (e == 1 || M > kSignGemvMaxM) && !(has_bias && fill_to > R) && fill_to <= L.RT * 16;
+  // several terms (MDBF): one unit size, and pre scales on all of them or none
+  int nu_min = L.NU;
+  for (int i = 1; i < n_terms && p.use; ++i) {
+    const SignLayout Li = make_sign_layout(R, terms[i].Kd);
+    p.use = Li.UK == L.UK && (terms[i].pre != nullptr) == (terms[0].pre != nullptr);
+    if (Li.NU < nu_min) nu_min = Li.NU;
+  }
   if (!p.use) return p;
   p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  const int nkb = L.NU * L.UK, wgs = (L.RT + 3) / 4;
+  const int nkb = nu_min * L.UK, wgs = (L.RT + 3) / 4 * n_terms;  // workgroups per split
   const int es = oc::knob("OC_SIGN_STREAM_S", 0);
   int S = es > 0 ? es : (oc_device_cus() + wgs - 1) / wgs;
   if (es <= 0) {
     if (S > 8) S = 8;
     if (S > nkb / 4) S = nkb / 4;
-    // column workgroups that already cover 3/4 of the CUs: no split, no
-    // reduce launch (up_proj's output stage at M = 32: 23.8 -> 21.5 us)
+    // column workgroups that already cover 3/4 of the CUs: no split (one
+    // term: no reduce launch; up_proj's output stage at M = 32: 23.8 -> 21.5 us)
     if (4 * wgs >= 3 * oc_device_cus()) S = 1;
   }
-  if (S > L.NU) S = L.NU;
+  if (S > nu_min) S = nu_min;
   if (S < 1) S = 1;
-  p.ups = (L.NU + S - 1) / S;
-  p.S = (L.NU + p.ups - 1) / p.ups;
-  p.bytes = p.S > 1 ? align256((size_t)p.S * M * L.RT * 16 * 4) : 0;
+  p.S = S;
+  p.T = n_terms;
+  p.bytes = S * n_terms > 1 ? align256((size_t)S * n_terms * M * L.RT * 16 * 4) : 0;
   return p;
 }
 
@@ -674,7 +699,7 @@ constexpr int sign_stream_kps(int mb) { return mb <= 2 ? 2 : 1; }
 
 template <int UK, bool BF16>
 int launch_sign_stream_uk(const SignStreamArgs& a, int mb, bool pre, hipStream_t st) {
-  const dim3 grid((a.RT + 3) / 4, a.S), block(256);
+  const dim3 grid((a.RT + 3) / 4, a.S * a.T), block(256);
   const size_t lds = (size_t)2 * 16 * mb * (sign_stream_kps(mb) * 128 + 8) * 2;
 #define OC_SS(MB_)                                                                                         \
   if (mb == MB_) {                                                                                         \
@@ -696,40 +721,45 @@ int launch_sign_stream(const SignStreamArgs& a, int uk, int mb, bool pre, hipStr
   return launch_sign_stream_uk<1, BF16>(a, mb, pre, st);
 }
 
-int sign_stream(const oc_sign_term& T, int M, int R, bool bf16, const void* bias, void* out, int ld_out,
+int sign_stream(const oc_sign_term* terms, int M, int R, bool bf16, const void* bias, void* out, int ld_out,
                 int fill_to, const SignStreamPlan& p, void* workspace, size_t ws_bytes, hipStream_t st) {
   OC_REQUIRE(ws_bytes >= p.bytes && (p.bytes == 0 || workspace), OC_ERR_WORKSPACE,
              "workspace of %zu bytes is smaller than the %zu required", ws_bytes, p.bytes);
-  const SignLayout L = make_sign_layout(R, T.Kd);
+  const SignLayout L = make_sign_layout(R, terms[0].Kd);
+  const int parts = p.S * p.T;
   SignStreamArgs a = {};
-  a.sg = (const uint32_t*)T.packed;
-  a.in = (const uint16_t*)T.in;
-  a.pre = (const uint16_t*)T.pre;
-  a.post = (const uint16_t*)T.post;
-  a.bias = p.S == 1 ? (const uint16_t*)bias : nullptr;
+  for (int i = 0; i < p.T; ++i) {
+    const oc_sign_term& T = terms[i];
+    a.sg[i] = (const uint32_t*)T.packed;
+    a.in[i] = (const uint16_t*)T.in;
+    a.pre[i] = (const uint16_t*)T.pre;
+    a.post[i] = (const uint16_t*)T.post;
+    a.ld_in[i] = T.ld_in;
+    a.Kd[i] = T.Kd;
+    a.NU[i] = make_sign_layout(R, T.Kd).NU;
+  }
+  a.bias = parts == 1 ? (const uint16_t*)bias : nullptr;
   a.out = (uint16_t*)out;
   a.partial = (float*)workspace;
-  a.ld_in = T.ld_in;
   a.ld_out = ld_out;
   a.M = M;
-  a.Kd = T.Kd;
   a.R = R;
   a.RT = L.RT;
-  a.NU = L.NU;
-  a.ups = p.ups;
   a.S = p.S;
+  a.T = p.T;
   a.fill_to = fill_to;
   a.N_pad = L.RT * 16;
-  const bool pre = T.pre != nullptr;
+  const bool pre = terms[0].pre != nullptr;
   const int rc = bf16 ? launch_sign_stream<true>(a, L.UK, p.mb, pre, st)
                 : launch_sign_stream<false>(a, L.UK, p.mb, pre, st);
-  if (rc || p.S == 1) return rc;
+  if (rc || parts == 1) return rc;
+  // the terms' and splits' fp32 partials, added in (term, split) order
   const dim3 g((fill_to + 255) / 256, M);
   if (bf16)
-    hipLaunchKernelGGL(k_sign_reduce<true>, g, dim3(256), 0, st, a.partial, p.S, M, fill_to, a.N_pad, R,
+    hipLaunchKernelGGL(k_sign_reduce<true>, g, dim3(256), 0, st, a.partial, parts, M, fill_to, a.N_pad, R,
                        (const uint16_t*)bias, (uint16_t*)out, ld_out);
   else
-    hipLaunchKernelGGL(k_sign_reduce<false>, g, dim3(256), 0, st, a.partial, p.S, M, fill_to, a.N_pad, R,
+    hipLaunchKernelGGL(k_sign_reduce<false>, g, dim3(256), 0, st, a.partial, parts, M, fill_to, a.N_pad, R,
                        (const uint16_t*)bias, (uint16_t*)out, ld_out);
   OC_HIP(hipGetLastError());
   return 0;
@@ -941,7 +971,7 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
   {
     const SignStreamPlan sp = plan_sign_stream(terms, n_terms, M, R, bias != nullptr, fill_to);
     if (sp.use)
-      return sign_stream(terms[0], M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to, sp, workspace,
+      return sign_stream(terms, M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to, sp, workspace,
                          ws_bytes, (hipStream_t)stream);
   }
   if (M >= sign_gemm_min_m())

@@ -217,15 +217,24 @@ def test_mdbf_mid_m_two_paths(dev, m):
     assert _rel(y, ref) <= 2e-3, _rel(y, ref)
 
 
-# The large-M sign GEMM sums several terms in one accumulation, each term's per-column post scale
-# folded into its +-1 operand (sign flips where the scale is negative, +1 without a post vector),
-# with K-split pieces over the concatenated k-blocks; without a bias the zero columns R..fill_to
-# come out of the GEMM itself.
-@pytest.mark.parametrize("m", [40, 140])
+# Several terms summed into one output, signed per-column post scales (+1 without a post vector).
+# The large-M sign GEMM (m = 140, and path "gemm") sums them in one accumulation, each term's post
+# scale folded into its +-1 operand, with K-split pieces over the concatenated k-blocks; without a
+# bias the zero columns R..fill_to come out of the GEMM itself.  The streaming sign kernel (m = 40:
+# "auto", and "s2" with two K splits per term) runs the terms side by side, each writing its own
+# post-scaled fp32 partial, which k_sign_reduce adds in term order with the bias (a call with a bias
+# and zero columns takes the GEMM path).
+@pytest.mark.parametrize("m,path", [(40, "auto"), (40, "gemm"), (40, "s2"), (140, "auto")])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-@pytest.mark.parametrize("n_terms,with_bias", [(1, False), (3, False), (4, True)])
-def test_sign_gemm_terms_signed_scales(dev, m, dtype, n_terms, with_bias):
-    R, fill_to, ld_out = 530, 536, 544
+@pytest.mark.parametrize("n_terms,with_bias,fill", [(1, False, True), (2, False, True), (3, False, True),
+                                                    (4, True, True), (4, True, False)])
+def test_sign_gemm_terms_signed_scales(dev, m, path, dtype, n_terms, with_bias, fill, plan):
+    if path == "gemm":
+        plan("OC_SIGN_STREAM", 0)
+    elif path == "s2":
+        plan("OC_SIGN_STREAM_S", 2)
+    R, ld_out = 530, 544
+    fill_to = 536 if fill else R
     kds = [300, 260, 330, 270][:n_terms]
     td = torch.float16 if dtype == "fp16" else torch.bfloat16
     rng = np.random.default_rng(40 + n_terms + m)
