@@ -260,10 +260,12 @@ def report_moe(dev, bits=4, gs=128, routings=16):
 
 def _time_graph(launch, copies, iters, warm=2):
     """µs per launch: `iters` launches (launch(i) uses copy i % copies) in one HIP graph, the median of
-    three timed replays."""
+    three timed replays.  Every copy runs once before the capture (as every layer of a served model
+    has run once): a layer's first call builds its cached operands (the DBF/MDBF scale vectors in the
+    activation dtype), which must not be captured into the graph and re-run on each replay."""
     import torch
 
-    for i in range(warm):
+    for i in range(max(warm, copies)):
         launch(i)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()

@@ -73,6 +73,9 @@ def _vec(t: Optional[torch.Tensor], dtype: torch.dtype, n: int, cache: Dict, key
     k = (key, dtype)
     v = cache.get(k)
     if v is None:
+        if _capturing(t):
+            raise RuntimeError(f"scale vector {key} built under HIP graph capture (it would live in the "
+                               "graph's private pool); prepare the layer with dbf_prepare/mdbf_prepare_path")
         src = t.reshape(-1)
         if src.numel() != n:
             raise ValueError(f"scale vector {key} has {src.numel()} entries, expected {n}")
@@ -80,6 +83,19 @@ def _vec(t: Optional[torch.Tensor], dtype: torch.dtype, n: int, cache: Dict, key
         v[:n].copy_(src)
         cache[k] = v
     return v
+
+
+def _capturing(t: torch.Tensor) -> bool:
+    return t.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
+def _fill_vecs(cache: Dict, items) -> None:
+    """Build a layer's cached scale vectors for both activation dtypes at prepare time, so that no
+    forward call creates them: one created during HIP graph capture would live in the graph's
+    private memory pool (and the capture would re-run its fill on every replay)."""
+    for dt in _DT:
+        for t, n, key in items:
+            _vec(t, dt, n, cache, key)
 
 
 def sign_gemm(terms, M: int, R: int, dtype: torch.dtype, out: torch.Tensor, ld_out: int,
@@ -126,7 +142,9 @@ def dbf_prepare(s0, bp1, s2, bp3, s4, in_features: int, mid: int, out_features: 
     """One DBF part: scaling0 [K], bp1 (r x K), scaling2 [r], bp3 (N x r), scaling4 [N]."""
     S2 = sign_prepare(bp1, mid, in_features)
     S1 = sign_prepare(bp3, out_features, mid)
-    return DBFPart(s0, s2, s4, S2, S1, in_features, mid, out_features)
+    p = DBFPart(s0, s2, s4, S2, S1, in_features, mid, out_features)
+    _fill_vecs(p._cache, [(s0, in_features, "s0"), (s2, mid, "s2"), (s4, out_features, "s4")])
+    return p
 
 
 def dbf_forward(x: torch.Tensor, parts: List[DBFPart], bias: Optional[torch.Tensor] = None,
@@ -186,7 +204,10 @@ def mdbf_prepare_path(a_packed, a_shape, b_packed, b_shape, a_amp, b_amp, qu_amp
     def tr(t, d):
         return t.reshape(d, l).t().contiguous()
 
-    return MDBFPath(A, B, tr(a_amp, n), tr(b_amp, m), tr(qu_amp, r), tr(qv_amp, r), n, r, m, l)
+    p = MDBFPath(A, B, tr(a_amp, n), tr(b_amp, m), tr(qu_amp, r), tr(qv_amp, r), n, r, m, l)
+    _fill_vecs(p._cache, [v for k in range(l) for v in ((p.B_amp[k], m, f"b{k}"), (p.Q_V[k], r, f"qv{k}"),
+                                                          (p.Q_U[k], r, f"qu{k}"), (p.A_amp[k], n, f"a{k}"))])
+    return p
 
 
 def mdbf_forward(x: torch.Tensor, paths: List[MDBFPath], bias: Optional[torch.Tensor] = None) -> torch.Tensor:

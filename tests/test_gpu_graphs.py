@@ -95,3 +95,28 @@ def test_moe_graph(dev, m):
                 torch.softmax(torch.randn(m, k, generator=gen), dim=-1)]
 
     _replays(dev, inputs, lambda b: moe.moe_forward(b[0], b[1], b[2], ex, "silu"))
+
+
+def test_dbf_first_call_captured(dev):
+    """A freshly prepared DBF layer and MDBF path whose first call is made under capture: every
+    operand the forward reads was built at prepare time (none in the graph's private pool), so the
+    replays and later eager calls (after the graph is freed) equal a fresh eager call."""
+    c = synth.dbf_case("d", 1024, 2048, 1.0, seed=8).to(dev)
+    part = dbf_ops.dbf_prepare(c.s0, c.bp1, c.s2, c.bp3, c.s4, c.in_features, c.mid, c.out_features)
+    n_, k_ = c.out_features, c.in_features
+    path = dbf_ops.mdbf_prepare_path(c.bp3, (n_, c.mid), c.bp1, (c.mid, k_), c.s4.view(n_, 1),
+                                     c.s0.view(k_, 1), c.s2.view(c.mid, 1),
+                                     torch.ones((c.mid, 1), dtype=torch.float16, device=dev))
+    for m in (1, 32):
+        x = synth.activations(m, 1024, torch.float16, seed=90 + m).to(dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = dbf_ops.dbf_forward(x, [part])
+            y2 = dbf_ops.mdbf_forward(x, [path, path])
+        g.replay()
+        torch.cuda.synchronize()
+        got, got2 = y.clone(), y2.clone()
+        del g, y, y2
+        torch.cuda.empty_cache()
+        assert torch.equal(got, dbf_ops.dbf_forward(x, [part]))
+        assert torch.equal(got2, dbf_ops.mdbf_forward(x, [path, path]))
