@@ -246,8 +246,8 @@ typedef struct {
   int ld_in;
 } oc_sign_term;
 
-/* Device workspace bytes oc_sign_gemm needs for these terms at M rows (host only).  0 at M <= 16
- * (the GEMV path needs none); at 16 < M <= 64 the streaming kernel's fp32 partials (one per term
+/* Device workspace bytes oc_sign_gemm needs for these terms at M rows (host only).  0 at M <= 12
+ * (the GEMV path needs none); at 13 <= M <= 64 the streaming kernel's fp32 partials (one per term
  * and K split, when there is more than one), or what the GEMM path needs if larger; above 64 rows
  * the pre-scaled inputs RNE(in * pre) of the terms that have a pre scale plus the fp32 partial
  * tiles of the K-split pieces (all terms are summed in one accumulation). */

@@ -426,7 +426,7 @@ __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int 
 }
 
 // ---------------------------------------------------------------------------
-// 16 < M <= 64: one wave per 16-row output tile streams its share of a term's
+// 13 <= M <= 64: one wave per 16-row output tile streams its share of a term's
 // k-blocks; the workgroup's 4 waves (4 consecutive tiles) share x, staged in a
 // two-buffer LDS ring (KPS = 2 k-blocks per buffer and barrier up to 32 rows,
 // 1 at 64) with the pre scale applied on the way (RNE(in * pre), the
@@ -446,6 +446,9 @@ __global__ void k_zero_cols(uint16_t* __restrict__ out, int ld_out, int c0, int 
 // partial[term S + split][m][n] and k_sign_reduce adds them in that order.
 // ---------------------------------------------------------------------------
 constexpr int kSignStreamMaxM = 64;
+// from 13 rows (one 16-row block) the streaming kernel beats the GEMV at config 3 (M = 16: DBF
+// down 21.1 -> 19.5 us, MDBF down 41.6 -> 33.3); at M = 8 the GEMV is faster (16.8 vs 19.1)
+constexpr int kSignStreamMinM = 13;
 
 struct SignStreamArgs {
   // per term (T of them): sign layout, input [M, ld_in], pre scale [round8(Kd)] zero-padded (all
@@ -654,7 +657,7 @@ struct SignStreamPlan {
   size_t bytes;
 };
 
-// The streaming sign kernel serves 16 < M <= 64 (OC_SIGN_STREAM = 0 turns it
+// The streaming sign kernel serves 13 <= M <= 64 (OC_SIGN_STREAM = 0 turns it
 // off, 1 forces it for any M <= 64), one term or up to four; K splits of each
 // term on unit boundaries: enough workgroups (all terms') for one per CU, at
 // most 8, at least 4 k-blocks each, none when the column workgroups alone cover
@@ -665,7 +668,7 @@ SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, i
   const int e = oc::knob("OC_SIGN_STREAM", -1);
   const SignLayout L = make_sign_layout(R, terms[0].Kd);
   p.use = n_terms >= 1 && n_terms <= kMaxTerms && e != 0 && M <= kSignStreamMaxM &&
-          (e == 1 || M > kSignGemvMaxM) && !(has_bias && fill_to > R) && fill_to <= L.RT * 16;
+          (e == 1 || M >= kSignStreamMinM) && !(has_bias && fill_to > R) && fill_to <= L.RT * 16;
   // several terms (MDBF): one unit size, and pre scales on all of them or none
   int nu_min = L.NU;
   for (int i = 1; i < n_terms && p.use; ++i) {
