@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 6
+#define OC_ABI_VERSION 7
 
 enum {
   OC_OK = 0,
@@ -263,6 +263,21 @@ size_t oc_sign_workspace_bytes(const oc_sign_term* terms, int n_terms, int M, in
 int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R, int act_dtype,
                  const void* bias, void* out, int ld_out, int fill_to, void* workspace,
                  size_t ws_bytes, void* stream);
+
+/* Device workspace bytes oc_sign_gemm_batch needs for these problems at M rows (host only). */
+size_t oc_sign_batch_workspace_bytes(const oc_sign_term* problems, int n_problems, int M, int R);
+
+/* n_problems <= 4 independent single-term problems with the same M, R, ld_out and fill_to:
+ * outs[p][m, n] = problems[p] above (no bias), rounded to act_dtype, zero for R <= n < fill_to.
+ * MDBF's per-path rank stages (MultipathMDBFLinear.forward, mdbf_layer.py:412-420: each path's
+ * u = Q_V * (B @ (B_amp * x)) on the same x) in one launch where they share a unit size and all
+ * or none have a pre scale: the sign GEMV at M <= 12 (blockIdx.y = problem), the streaming sign
+ * kernel at 13 <= M <= 64 (+ one reduce launch when K is split); otherwise one oc_sign_gemm per
+ * problem.  Each output equals oc_sign_gemm on that problem alone, bit for bit.  workspace:
+ * oc_sign_batch_workspace_bytes() bytes (NULL when 0); no allocation, no host synchronisation. */
+int oc_sign_gemm_batch(const oc_sign_term* problems, int n_problems, int M, int R, int act_dtype,
+                       void* const* outs, int ld_out, int fill_to, void* workspace, size_t ws_bytes,
+                       void* stream);
 
 /* ---------------------------------------------------------------- online Hadamard ---------- */
 

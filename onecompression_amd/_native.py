@@ -53,9 +53,11 @@ SIGNATURES = {
     "oc_hadamard_block": (c_int, [c_int, P]),
     "oc_hadamard": (c_int, [P, c_int, c_int, c_int, P, c_int, c_int, c_int, P, c_int, P]),
     "oc_sign_gemm": (c_int, [P, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, c_size_t, P]),
+    "oc_sign_batch_workspace_bytes": (c_size_t, [P, c_int, c_int, c_int]),
+    "oc_sign_gemm_batch": (c_int, [P, c_int, c_int, c_int, c_int, P, c_int, c_int, P, c_size_t, P]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 OC_DTYPE_F16, OC_DTYPE_BF16 = 0, 1
 OC_HAD_ROUND_FP32, OC_HAD_ROUND_ONCE, OC_HAD_ROUND_STAGES = 0, 1, 2
 OC_ZERO_RAW, OC_ZERO_V1, OC_ZERO_V2 = 0, 1, 2

@@ -103,10 +103,19 @@ struct TermArgs {
 struct SignArgs {
   TermArgs t[kMaxTerms];
   int n_terms;
-  uint16_t* out;
+  // outs[0]; a batch of independent problems (term p into outs[p], no bias) runs p = blockIdx.y
+  uint16_t* outs[kMaxTerms];
   const uint16_t* bias;
   int ld_out, M, R, RT, fill_to, W;
+  int batch;  // problems (grid.y; 1 unless batched)
 };
+
+// element t of a per-term argument array (t uniform; a compare chain, not a
+// dynamic index into the kernel arguments)
+template <class V>
+__device__ __forceinline__ V term_pick(int t, const V (&v)[kMaxTerms]) {
+  return t == 0 ? v[0] : (t == 1 ? v[1] : (t == 2 ? v[2] : v[3]));
+}
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t mul2(uint32_t a, uint32_t b) {
@@ -149,12 +158,28 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
   const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
   const uint32_t smask = oc_opaque(0x80008000u);
   const int M = a.M;
+  // problem of a batched launch (single-term kernels only; 0 otherwise) and its output
+  const int pb = MULTI ? 0 : blockIdx.y;
+  // field by field with constant indices (a dynamic index into the argument structs would copy
+  // them to scratch)
+  TermArgs T0;
+#define OC_TF(f) (pb == 0 ? a.t[0].f : (pb == 1 ? a.t[1].f : (pb == 2 ? a.t[2].f : a.t[3].f)))
+  T0.sg = OC_TF(sg);
+  T0.in = OC_TF(in);
+  T0.pre = OC_TF(pre);
+  T0.post = OC_TF(post);
+  T0.ld_in = OC_TF(ld_in);
+  T0.Kd = OC_TF(Kd);
+  T0.NU = OC_TF(NU);
+  T0.UK = OC_TF(UK);
+#undef OC_TF
+  uint16_t* const out = term_pick(pb, a.outs);
 
   extern __shared__ __align__(16) uint8_t smem[];
   if (rt * 16 >= a.R) {  // padding tiles: zero-fill up to fill_to
     for (int e = threadIdx.x; e < M * 16; e += 64 * W) {
       const int m = e >> 4, c = rt * 16 + (e & 15);
-      if (c < a.fill_to) a.out[(size_t)m * a.ld_out + c] = 0;
+      if (c < a.fill_to) out[(size_t)m * a.ld_out + c] = 0;
     }
     return;
   }
@@ -174,8 +199,9 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
   uint16_t praw[kMaxTerms];
 #pragma unroll
   for (int q = 0; q < (MULTI ? kMaxTerms : 1); ++q) {
-    const bool ok = q < a.n_terms && a.t[q].post != nullptr && n < a.R;
-    praw[q] = __builtin_amdgcn_raw_buffer_load_b16(oc_rsrc(q < a.n_terms ? a.t[q].post : nullptr, (uint32_t)a.R * 2),
+    const uint16_t* post_q = q == 0 ? T0.post : (q < a.n_terms ? a.t[q].post : nullptr);
+    const bool ok = q < a.n_terms && post_q != nullptr && n < a.R;
+    praw[q] = __builtin_amdgcn_raw_buffer_load_b16(oc_rsrc(post_q, (uint32_t)a.R * 2),
                                                    ok ? (uint32_t)n * 2 : kOcOob, 0, 0);
   }
   const int ecol = rt * 16 + (threadIdx.x & 15);
@@ -186,7 +212,7 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
   // MULTI: several terms one after another (the pipeline drains between
   // them); a single term is compiled without the loop (exact load waits).
   for (int t = 0; t < (MULTI ? a.n_terms : 1); ++t) {
-    const TermArgs T = a.t[t];
+    const TermArgs T = (MULTI && t > 0) ? a.t[t] : T0;
     const int n_my = wave < T.NU ? (T.NU - wave + W - 1) / W : 0;
     uint32_t sbuf[D][UK];
     oc_u4 xbuf[D][XCH];
@@ -277,7 +303,7 @@ __global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
     const int ln = e & 63, r = e >> 6;
     const int m = 4 * (ln >> 4) + r, c = rt * 16 + (ln & 15);
     if (m < M && c < a.fill_to)
-      a.out[(size_t)m * a.ld_out + c] = c < a.R ? (BF16 ? oc_f2bf(v + bval) : oc_f2h(v + bval)) : (uint16_t)0;
+      out[(size_t)m * a.ld_out + c] = c < a.R ? (BF16 ? oc_f2bf(v + bval) : oc_f2h(v + bval)) : (uint16_t)0;
   }
 }
 
@@ -302,7 +328,7 @@ int launch_sign_x(const SignArgs& a, bool pre, int rt_grid, hipStream_t st) {
   const size_t xb = slot * a.W;
   const size_t rb = (size_t)a.W * 4 * 64 * 4;
   const size_t lds = ((xb > rb ? xb : rb) + 15) / 16 * 16;
-  const dim3 g(rt_grid), b(64 * a.W);
+  const dim3 g(rt_grid, a.batch > 1 ? a.batch : 1), b(64 * a.W);
   if (a.n_terms > 1) {
     if (pre) hipLaunchKernelGGL((k_sign_gemv<UK, XCH, true, true, BF16>), g, b, lds, st, a);
     else hipLaunchKernelGGL((k_sign_gemv<UK, XCH, false, true, BF16>), g, b, lds, st, a);
@@ -458,18 +484,14 @@ struct SignStreamArgs {
   const uint16_t* pre[kMaxTerms];
   const uint16_t* post[kMaxTerms];
   int ld_in[kMaxTerms], Kd[kMaxTerms], NU[kMaxTerms];
-  const uint16_t* bias;   // [R] or null (T S == 1 only)
-  uint16_t* out;          // [M, ld_out]
-  float* partial;         // [T S, M, N_pad] when T S > 1
-  int ld_out, M, R, RT, S, T, fill_to, N_pad;
+  const uint16_t* bias;   // [R] or null (one output, T S == 1 only)
+  // summed (separate = 0): every term into outs[0]; separate = 1: term t into outs[t] (a batch of
+  // independent problems, no bias)
+  uint16_t* outs[kMaxTerms];
+  float* partial;         // [T S, M, N_pad] when the outputs take more than one partial
+  int ld_out, M, R, RT, S, T, fill_to, N_pad, separate;
 };
 
-// element t of a per-term argument array (t uniform; a compare chain, not a
-// dynamic index into the kernel arguments)
-template <class V>
-__device__ __forceinline__ V term_pick(int t, const V (&v)[kMaxTerms]) {
-  return t == 0 ? v[0] : (t == 1 ? v[1] : (t == 2 ? v[2] : v[3]));
-}
 
 template <int MB, int UK, int KPS, bool PRE, bool BF16>
 __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) {
@@ -617,7 +639,8 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   if (rt >= a.RT || n >= a.fill_to) return;
   float ps = 0.f;  // columns R .. fill_to: zeros
   if (n < a.R) ps = post ? (BF16 ? oc_bf2f(post[n]) : oc_h2f(post[n])) : 1.f;
-  if (a.S * a.T > 1) {
+  uint16_t* const out = a.separate ? term_pick(t, a.outs) : a.outs[0];
+  if ((a.separate ? a.S : a.S * a.T) > 1) {
     float* pp = a.partial + (size_t)blockIdx.y * M * a.N_pad + n;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -634,27 +657,36 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 16 * i + 4 * kq + r;
-      if (m < M) a.out[(size_t)m * a.ld_out + n] = BF16 ? oc_f2bf(fmaf(yacc[i][r], ps, b)) : oc_f2h(fmaf(yacc[i][r], ps, b));
+      if (m < M) out[(size_t)m * a.ld_out + n] = BF16 ? oc_f2bf(fmaf(yacc[i][r], ps, b)) : oc_f2h(fmaf(yacc[i][r], ps, b));
     }
 }
 
-// out[m, n] = sum over splits (in split order) of partial[s, m, n] (+ bias[n] for n < R), n < ncols.
+// outs[z][m, n] = sum over s < S (in order) of partial[z S + s, m, n] (+ bias[n] for n < R), n < ncols;
+// z = blockIdx.z (one output, z = 0; a batch of independent problems, one z per problem).
+struct SignReduceArgs {
+  const float* partial;
+  const uint16_t* bias;
+  uint16_t* outs[kMaxTerms];
+  int S, M, ncols, N_pad, R, ld_out;
+};
+
 template <bool BF16>
-__global__ void k_sign_reduce(const float* __restrict__ partial, int S, int M, int ncols, int N_pad, int R,
-                              const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int ld_out) {
+__global__ void k_sign_reduce(const SignReduceArgs a) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  const int m = blockIdx.y;
-  if (n >= ncols) return;
+  const int m = blockIdx.y, z = blockIdx.z;
+  if (n >= a.ncols) return;
+  const float* part = a.partial + (size_t)z * a.S * a.M * a.N_pad;
   float o = 0.f;
-  for (int s = 0; s < S; ++s) o += partial[((size_t)s * M + m) * N_pad + n];
-  if (bias && n < R) o += BF16 ? oc_bf2f(bias[n]) : oc_h2f(bias[n]);
-  out[(size_t)m * ld_out + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
+  for (int s = 0; s < a.S; ++s) o += part[((size_t)s * a.M + m) * a.N_pad + n];
+  if (a.bias && n < a.R) o += BF16 ? oc_bf2f(a.bias[n]) : oc_h2f(a.bias[n]);
+  term_pick(z, a.outs)[(size_t)m * a.ld_out + n] = BF16 ? oc_f2bf(o) : oc_f2h(o);
 }
 
 struct SignStreamPlan {
   bool use;
-  int mb, S, T;  // row blocks, K splits per term, terms (T S > 1: fp32 partials + k_sign_reduce)
-  size_t bytes;
+  int mb, S, T;   // row blocks, K splits per term, terms
+  bool separate;  // terms into their own outputs (a batch of problems)
+  size_t bytes;   // fp32 partials when an output takes more than one (+ k_sign_reduce)
 };
 
 // The streaming sign kernel serves 13 <= M <= 64 (OC_SIGN_STREAM = 0 turns it
@@ -663,7 +695,7 @@ struct SignStreamPlan {
 // most 8, at least 4 k-blocks each, none when the column workgroups alone cover
 // 3/4 of the CUs (OC_SIGN_STREAM_S forces S).
 SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, int R, bool has_bias,
-                                int fill_to) {
+                                int fill_to, bool separate = false) {
   SignStreamPlan p = {};
   const int e = oc::knob("OC_SIGN_STREAM", -1);
   const SignLayout L = make_sign_layout(R, terms[0].Kd);
@@ -692,7 +724,9 @@ SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, i
   if (S < 1) S = 1;
   p.S = S;
   p.T = n_terms;
-  p.bytes = S * n_terms > 1 ? align256((size_t)S * n_terms * M * L.RT * 16 * 4) : 0;
+  p.separate = separate;
+  const bool parts = separate ? S > 1 : S * n_terms > 1;
+  p.bytes = parts ? align256((size_t)S * n_terms * M * L.RT * 16 * 4) : 0;
   return p;
 }
 
@@ -724,12 +758,13 @@ int launch_sign_stream(const SignStreamArgs& a, int uk, int mb, bool pre, hipStr
   return launch_sign_stream_uk<1, BF16>(a, mb, pre, st);
 }
 
-int sign_stream(const oc_sign_term* terms, int M, int R, bool bf16, const void* bias, void* out, int ld_out,
-                int fill_to, const SignStreamPlan& p, void* workspace, size_t ws_bytes, hipStream_t st) {
+// outs: the one output (outs[0]), or one per term with p.separate
+int sign_stream(const oc_sign_term* terms, int M, int R, bool bf16, const void* bias, void* const* outs,
+                int ld_out, int fill_to, const SignStreamPlan& p, void* workspace, size_t ws_bytes, hipStream_t st) {
   OC_REQUIRE(ws_bytes >= p.bytes && (p.bytes == 0 || workspace), OC_ERR_WORKSPACE,
              "workspace of %zu bytes is smaller than the %zu required", ws_bytes, p.bytes);
   const SignLayout L = make_sign_layout(R, terms[0].Kd);
-  const int parts = p.S * p.T;
+  const int parts = p.separate ? p.S : p.S * p.T;  // partials per output
   SignStreamArgs a = {};
   for (int i = 0; i < p.T; ++i) {
     const oc_sign_term& T = terms[i];
@@ -740,9 +775,9 @@ int sign_stream(const oc_sign_term* terms, int M, int R, bool bf16, const void* 
     a.ld_in[i] = T.ld_in;
     a.Kd[i] = T.Kd;
     a.NU[i] = make_sign_layout(R, T.Kd).NU;
+    a.outs[i] = (uint16_t*)outs[p.separate ? i : 0];
   }
   a.bias = parts == 1 ? (const uint16_t*)bias : nullptr;
-  a.out = (uint16_t*)out;
   a.partial = (float*)workspace;
   a.ld_out = ld_out;
   a.M = M;
@@ -752,18 +787,25 @@ int sign_stream(const oc_sign_term* terms, int M, int R, bool bf16, const void* 
   a.T = p.T;
   a.fill_to = fill_to;
   a.N_pad = L.RT * 16;
+  a.separate = p.separate ? 1 : 0;
   const bool pre = terms[0].pre != nullptr;
   const int rc = bf16 ? launch_sign_stream<true>(a, L.UK, p.mb, pre, st)
                 : launch_sign_stream<false>(a, L.UK, p.mb, pre, st);
   if (rc || parts == 1) return rc;
-  // the terms' and splits' fp32 partials, added in (term, split) order
-  const dim3 g((fill_to + 255) / 256, M);
-  if (bf16)
-    hipLaunchKernelGGL(k_sign_reduce<true>, g, dim3(256), 0, st, a.partial, parts, M, fill_to, a.N_pad, R,
-                       (const uint16_t*)bias, (uint16_t*)out, ld_out);
-  else
-    hipLaunchKernelGGL(k_sign_reduce<false>, g, dim3(256), 0, st, a.partial, parts, M, fill_to, a.N_pad, R,
-                       (const uint16_t*)bias, (uint16_t*)out, ld_out);
+  // each output's fp32 partials, added in (term, split) order
+  SignReduceArgs r = {};
+  r.partial = a.partial;
+  r.bias = (const uint16_t*)bias;
+  for (int i = 0; i < kMaxTerms; ++i) r.outs[i] = a.outs[p.separate && i < p.T ? i : 0];
+  r.S = parts;
+  r.M = M;
+  r.ncols = fill_to;
+  r.N_pad = a.N_pad;
+  r.R = R;
+  r.ld_out = ld_out;
+  const dim3 g((fill_to + 255) / 256, M, p.separate ? p.T : 1);
+  if (bf16) hipLaunchKernelGGL(k_sign_reduce<true>, g, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL(k_sign_reduce<false>, g, dim3(256), 0, st, r);
   OC_HIP(hipGetLastError());
   return 0;
 }
@@ -974,13 +1016,14 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
   {
     const SignStreamPlan sp = plan_sign_stream(terms, n_terms, M, R, bias != nullptr, fill_to);
     if (sp.use)
-      return sign_stream(terms, M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to, sp, workspace,
+      return sign_stream(terms, M, R, act_dtype == OC_DTYPE_BF16, bias, &out, ld_out, fill_to, sp, workspace,
                          ws_bytes, (hipStream_t)stream);
   }
   if (M >= sign_gemm_min_m())
     return sign_gemm_large(terms, n_terms, M, R, act_dtype == OC_DTYPE_BF16, bias, out, ld_out, fill_to,
                            workspace, ws_bytes, (hipStream_t)stream);
   a.n_terms = n_terms;
+  a.batch = 1;
   a.bias = (const uint16_t*)bias;
   a.R = R;
   a.RT = (R + 15) / 16;
@@ -997,7 +1040,7 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
     SignArgs c = a;
     c.M = M - m0 < kSignGemvMaxM ? M - m0 : kSignGemvMaxM;
     c.W = sign_waves(a.RT, nu_min, c.M, uk);
-    c.out = (uint16_t*)out + (size_t)m0 * ld_out;
+    c.outs[0] = (uint16_t*)out + (size_t)m0 * ld_out;
     for (int i = 0; i < n_terms; ++i) c.t[i].in = a.t[i].in + (size_t)m0 * a.t[i].ld_in;
     int rc;
     if (uk == 4)
@@ -1006,6 +1049,90 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
       rc = bf16 ? launch_sign<2, true>(c, pre, rt_grid, st) : launch_sign<2, false>(c, pre, rt_grid, st);
     else
       rc = bf16 ? launch_sign<1, true>(c, pre, rt_grid, st) : launch_sign<1, false>(c, pre, rt_grid, st);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+extern "C" size_t oc_sign_batch_workspace_bytes(const oc_sign_term* terms, int n_problems, int M, int R) {
+  if (!terms || n_problems < 1 || n_problems > kMaxTerms || R <= 0) return 0;
+  for (int i = 0; i < n_problems; ++i)
+    if (terms[i].Kd <= 0) return 0;
+  const SignStreamPlan sp = plan_sign_stream(terms, n_problems, M, R, false, R, true);
+  if (sp.use) return sp.bytes;
+  size_t w = 0;  // the GEMV path needs none; otherwise one problem at a time
+  for (int i = 0; i < n_problems; ++i) {
+    const size_t b = oc_sign_workspace_bytes(&terms[i], 1, M, R);
+    w = b > w ? b : w;
+  }
+  return w;
+}
+
+extern "C" int oc_sign_gemm_batch(const oc_sign_term* terms, int n_problems, int M, int R, int act_dtype,
+                                  void* const* outs, int ld_out, int fill_to, void* workspace, size_t ws_bytes,
+                                  void* stream) {
+  OC_REQUIRE(terms && outs, OC_ERR_INVALID, "null pointer");
+  OC_REQUIRE(n_problems >= 1 && n_problems <= kMaxTerms, OC_ERR_UNSUPPORTED, "n_problems=%d must be 1..%d",
+             n_problems, kMaxTerms);
+  OC_REQUIRE(M >= 0 && R > 0, OC_ERR_INVALID, "bad M=%d R=%d", M, R);
+  OC_REQUIRE(act_dtype == OC_DTYPE_F16 || act_dtype == OC_DTYPE_BF16, OC_ERR_UNSUPPORTED, "bad act_dtype %d",
+             act_dtype);
+  if (fill_to < R) fill_to = R;
+  OC_REQUIRE(ld_out >= fill_to, OC_ERR_SHAPE, "ld_out=%d < fill_to=%d", ld_out, fill_to);
+  bool one_launch = n_problems > 1;
+  int uk = 0;
+  for (int i = 0; i < n_problems; ++i) {
+    const oc_sign_term& T = terms[i];
+    OC_REQUIRE(outs[i] && T.packed && T.in, OC_ERR_INVALID, "problem %d: null pointer", i);
+    OC_REQUIRE(T.Kd > 0 && T.ld_in >= T.Kd && T.ld_in % 8 == 0, OC_ERR_SHAPE,
+               "problem %d: Kd=%d / ld_in=%d (ld_in must be >= Kd and a multiple of 8)", i, T.Kd, T.ld_in);
+    const SignLayout L = make_sign_layout(R, T.Kd);
+    one_launch = one_launch && (uk == 0 || uk == L.UK) && ((T.pre != nullptr) == (terms[0].pre != nullptr));
+    uk = L.UK;
+  }
+  if (M == 0) return 0;
+  const bool bf16 = act_dtype == OC_DTYPE_BF16;
+  hipStream_t st = (hipStream_t)stream;
+  if (one_launch) {
+    const SignStreamPlan sp = plan_sign_stream(terms, n_problems, M, R, false, fill_to, true);
+    if (sp.use) return sign_stream(terms, M, R, bf16, nullptr, outs, ld_out, fill_to, sp, workspace, ws_bytes, st);
+    if (M <= kSignGemvMaxM && M < sign_gemm_min_m()) {
+      // the single-term GEMV, blockIdx.y = problem
+      SignArgs a = {};
+      int nu_min = 1 << 30;
+      for (int i = 0; i < n_problems; ++i) {
+        const oc_sign_term& T = terms[i];
+        const SignLayout L = make_sign_layout(R, T.Kd);
+        a.t[i].sg = (const uint32_t*)T.packed;
+        a.t[i].in = (const uint16_t*)T.in;
+        a.t[i].pre = (const uint16_t*)T.pre;
+        a.t[i].post = (const uint16_t*)T.post;
+        a.t[i].ld_in = T.ld_in;
+        a.t[i].Kd = T.Kd;
+        a.t[i].NU = L.NU;
+        a.t[i].UK = L.UK;
+        a.outs[i] = (uint16_t*)outs[i];
+        nu_min = L.NU < nu_min ? L.NU : nu_min;
+      }
+      a.n_terms = 1;
+      a.batch = n_problems;
+      a.R = R;
+      a.RT = (R + 15) / 16;
+      a.fill_to = fill_to;
+      a.ld_out = ld_out;
+      a.M = M;
+      a.W = sign_waves(a.RT, nu_min, M, uk);
+      const int rt_grid = (fill_to + 15) / 16;
+      const bool pre = terms[0].pre != nullptr;
+      if (uk == 4) return bf16 ? launch_sign<4, true>(a, pre, rt_grid, st) : launch_sign<4, false>(a, pre, rt_grid, st);
+      if (uk == 2) return bf16 ? launch_sign<2, true>(a, pre, rt_grid, st) : launch_sign<2, false>(a, pre, rt_grid, st);
+      return bf16 ? launch_sign<1, true>(a, pre, rt_grid, st) : launch_sign<1, false>(a, pre, rt_grid, st);
+    }
+  }
+  // one problem at a time (the workspace is reused: the launches are ordered on the stream)
+  for (int i = 0; i < n_problems; ++i) {
+    const int rc = oc_sign_gemm(&terms[i], 1, M, R, act_dtype, nullptr, outs[i], ld_out, fill_to, workspace,
+                                ws_bytes, stream);
     if (rc) return rc;
   }
   return 0;

@@ -103,8 +103,15 @@ def sign_gemm(terms, M: int, R: int, dtype: torch.dtype, out: torch.Tensor, ld_o
     """Launch oc_sign_gemm; ``terms`` = list of (SignFactor, in [M, ld_in], pre, post)."""
     if not 1 <= len(terms) <= 4:
         raise NotImplementedError(f"{len(terms)} sign terms in one output; at most 4 are supported")
+    arr = _terms_array(terms, dtype)
+    nbytes = N.load().oc_sign_workspace_bytes(arr, len(terms), M, R)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=out.device) if nbytes else None
+    N.call("oc_sign_gemm", arr, len(terms), M, R, _DT[dtype], _ptr(bias), _ptr(out), ld_out,
+           fill_to, _ptr(ws), nbytes, _stream(out.device))
+
+
+def _terms_array(terms, dtype):
     arr = (OcSignTerm * len(terms))()
-    keep = []
     for i, (f, x, pre, post) in enumerate(terms):
         if x.dtype != dtype:
             raise TypeError("all terms must use the activation dtype")
@@ -112,11 +119,21 @@ def sign_gemm(terms, M: int, R: int, dtype: torch.dtype, out: torch.Tensor, ld_o
             raise ValueError("term input rows must be contiguous, 16-byte aligned, stride % 8 == 0")
         arr[i] = OcSignTerm(f.packed.data_ptr(), x.data_ptr(), 0 if pre is None else pre.data_ptr(),
                             0 if post is None else post.data_ptr(), f.Kd, x.stride(0))
-        keep.append(x)
-    nbytes = N.load().oc_sign_workspace_bytes(arr, len(terms), M, R)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=out.device) if nbytes else None
-    N.call("oc_sign_gemm", arr, len(terms), M, R, _DT[dtype], _ptr(bias), _ptr(out), ld_out,
-           fill_to, _ptr(ws), nbytes, _stream(out.device))
+    return arr
+
+
+def sign_gemm_batch(problems, M: int, R: int, dtype: torch.dtype, outs: List[torch.Tensor], ld_out: int,
+                    fill_to: int = 0) -> None:
+    """Launch oc_sign_gemm_batch: independent single-term problems (SignFactor, in, pre, post), problem p
+    into outs[p] (each [M, ld_out]); one launch where the problems share a unit size and pre presence."""
+    if not 1 <= len(problems) <= 4 or len(outs) != len(problems):
+        raise NotImplementedError(f"{len(problems)} problems in one batch; 1 to 4 with one output each")
+    arr = _terms_array(problems, dtype)
+    ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    nbytes = N.load().oc_sign_batch_workspace_bytes(arr, len(problems), M, R)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=outs[0].device) if nbytes else None
+    N.call("oc_sign_gemm_batch", arr, len(problems), M, R, _DT[dtype], ptrs, ld_out, fill_to, _ptr(ws), nbytes,
+           _stream(outs[0].device))
 
 
 def _ld(n: int) -> int:
@@ -221,14 +238,18 @@ def mdbf_forward(x: torch.Tensor, paths: List[MDBFPath], bias: Optional[torch.Te
     rows = x2.shape[0]
     dev, dt = x2.device, x2.dtype
     stage2 = []
-    us = []
-    for pi, p in enumerate(paths):
+    us = [torch.empty((rows, _ld(p.r)), dtype=dt, device=dev) for p in paths]
+    rank = [[(p.B, x2, _vec(p.B_amp[k], dt, mdim, p._cache, f"b{k}"), _vec(p.Q_V[k], dt, p.r, p._cache, f"qv{k}"))
+             for k in range(p.l)] for p in paths]
+    if len(paths) > 1 and all(p.l == 1 and p.r == paths[0].r for p in paths):
+        # the paths' rank stages are independent problems on the same x: one batched launch
+        r0 = paths[0].r
+        sign_gemm_batch([t[0] for t in rank], rows, r0, dt, us, us[0].stride(0), fill_to=us[0].stride(0))
+    else:
+        for p, terms, u in zip(paths, rank, us):
+            sign_gemm(terms, rows, p.r, dt, u, u.stride(0), fill_to=u.stride(0))
+    for p, u in zip(paths, us):
         c = p._cache
-        u = torch.empty((rows, _ld(p.r)), dtype=dt, device=dev)
-        terms = [(p.B, x2, _vec(p.B_amp[k], dt, mdim, c, f"b{k}"), _vec(p.Q_V[k], dt, p.r, c, f"qv{k}"))
-                 for k in range(p.l)]
-        sign_gemm(terms, rows, p.r, dt, u, u.stride(0), fill_to=u.stride(0))
-        us.append(u)
         stage2 += [(p.A, u, _vec(p.Q_U[k], dt, p.r, c, f"qu{k}"), _vec(p.A_amp[k], dt, ndim, c, f"a{k}"))
                    for k in range(p.l)]
     y = torch.empty((rows, ndim), dtype=dt, device=dev)

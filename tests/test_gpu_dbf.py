@@ -282,3 +282,41 @@ def test_sign_stream_forced_small_m(dev, m, plan):
     y = dbf_ops.dbf_forward(x.to(dev), [prep]).float().cpu().numpy()
     ref = od.dbf_forward(x.numpy(), s0, bp1, s2, bp3, s4, k, r, n)
     assert _rel(y, ref) <= 2e-3, _rel(y, ref)
+
+
+# oc_sign_gemm_batch: independent single-term problems (MDBF's per-path rank stages) in one launch —
+# the sign GEMV at M <= 12, the streaming kernel at 13 <= M <= 64 (with K splits and their per-problem
+# reduce at some M), one call per problem above 64 rows or when the problems' unit sizes differ.
+# Every output must equal oc_sign_gemm on its problem alone, bit for bit, and the oracle.
+@pytest.mark.parametrize("m", [1, 5, 13, 32, 64, 100])
+@pytest.mark.parametrize("n_prob,kds,with_pre", [(2, [1000, 1000], True), (3, [700, 700, 700], False),
+                                                 (2, [1000, 300], True)])  # last: unit sizes differ
+def test_sign_gemm_batch(dev, m, n_prob, kds, with_pre):
+    R, fill_to, ld_out = 530, 536, 544
+    td = torch.float16
+    rng = np.random.default_rng(70 + m + n_prob)
+    probs, refs = [], []
+    for i, kd in enumerate(kds):
+        signs = rng.choice([-1, 1], size=(R, kd))
+        f = dbf_ops.sign_prepare(_t(od.pack_binary(signs), dev), R, kd)
+        ldx = (kd + 7) // 8 * 8
+        x = torch.zeros((m, ldx), dtype=td)
+        x[:, :kd] = torch.randn(m, kd, generator=torch.Generator().manual_seed(80 + i)).to(td)
+        pre = None
+        if with_pre:
+            pre = torch.zeros(ldx, dtype=td)
+            pre[:kd] = (torch.rand(kd, generator=torch.Generator().manual_seed(90 + i)) + 0.5).to(td)
+        post = (torch.rand(R, generator=torch.Generator().manual_seed(100 + i)) + 0.25).to(td)
+        post[torch.rand(R, generator=torch.Generator().manual_seed(110 + i)) < 0.3] *= -1
+        xs = x[:, :kd].float() if pre is None else (x[:, :kd].float() * pre[:kd].float()).to(td).float()
+        refs.append((xs @ torch.from_numpy(signs).float().t()) * post.float())
+        probs.append((f, x.to(dev), None if pre is None else pre.to(dev), post.to(dev)))
+    outs = [torch.full((m, ld_out), 7.0, dtype=td, device=dev) for _ in probs]
+    dbf_ops.sign_gemm_batch(probs, m, R, td, outs, ld_out, fill_to=fill_to)
+    for i, (p, o, ref) in enumerate(zip(probs, outs, refs)):
+        one = torch.full((m, ld_out), 7.0, dtype=td, device=dev)
+        dbf_ops.sign_gemm([p], m, R, td, one, ld_out, fill_to=fill_to)
+        assert torch.equal(o, one), f"problem {i}: batched output differs from the single call"
+        oc = o.float().cpu()
+        assert _rel(oc[:, :R].numpy(), ref.numpy()) <= 2e-3
+        assert torch.all(oc[:, R:fill_to] == 0) and torch.all(oc[:, fill_to:] == 7.0)
