@@ -144,7 +144,7 @@ __device__ __forceinline__ uint32_t mul2(uint32_t a, uint32_t b) {
 // Input contract: in[m, k] for Kd <= k < round8(Kd) is finite, and zero
 // unless the term has a (zero-padded) pre scale.
 template <int UK, int XCH, bool PRE, bool MULTI, bool BF16>
-__global__ __launch_bounds__(1024) void k_sign_gemv(const SignArgs a) {
+__global__ __launch_bounds__(MULTI ? 512 : 1024) void k_sign_gemv(const SignArgs a) {
   constexpr int XW = UK * 128 + 8;  // halfs per staged x row
   constexpr int CPR = 16 * UK;      // 16-byte chunks per row and unit
   constexpr int VPU = UK + 4 * XCH + (PRE ? 4 : 0);
@@ -313,10 +313,13 @@ constexpr size_t kSignLds = 64 * 1024;
 // Waves per workgroup (4, 8 or 16): enough waves in total to cover the GPU
 // (the rank-side stage has few row tiles), no more than the units allow, and
 // an LDS x slot per wave.
-int sign_waves(int RT, int NU, int M, int UK) {
+int sign_waves(int RT, int NU, int M, int UK, bool multi) {
   const int e = oc::knob("OC_SIGN_W", 0);
   int w = (e == 4 || e == 8 || e == 16) ? e : (RT >= 768 ? 4 : (RT >= 384 ? 8 : 16));
   while (w > 4 && w > NU) w /= 2;
+  // several terms: at most 8 waves (the kernel's 512-thread bound leaves it 256 registers, where
+  // 1024 threads' 128 made it spill)
+  if (multi && w > 8) w = 8;
   const size_t slot = (size_t)M * (UK * 128 + 8) * 2;
   while (w > 4 && slot * w > kSignLds) w /= 2;
   return w;
@@ -1039,7 +1042,7 @@ extern "C" int oc_sign_gemm(const oc_sign_term* terms, int n_terms, int M, int R
   for (int m0 = 0; m0 < M; m0 += kSignGemvMaxM) {
     SignArgs c = a;
     c.M = M - m0 < kSignGemvMaxM ? M - m0 : kSignGemvMaxM;
-    c.W = sign_waves(a.RT, nu_min, c.M, uk);
+    c.W = sign_waves(a.RT, nu_min, c.M, uk, n_terms > 1);
     c.outs[0] = (uint16_t*)out + (size_t)m0 * ld_out;
     for (int i = 0; i < n_terms; ++i) c.t[i].in = a.t[i].in + (size_t)m0 * a.t[i].ld_in;
     int rc;
@@ -1121,7 +1124,7 @@ extern "C" int oc_sign_gemm_batch(const oc_sign_term* terms, int n_problems, int
       a.fill_to = fill_to;
       a.ld_out = ld_out;
       a.M = M;
-      a.W = sign_waves(a.RT, nu_min, M, uk);
+      a.W = sign_waves(a.RT, nu_min, M, uk, false);
       const int rt_grid = (fill_to + 15) / 16;
       const bool pre = terms[0].pre != nullptr;
       if (uk == 4) return bf16 ? launch_sign<4, true>(a, pre, rt_grid, st) : launch_sign<4, false>(a, pre, rt_grid, st);
