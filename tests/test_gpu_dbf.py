@@ -174,11 +174,12 @@ def test_sign_gemm_fill_and_bias(dev, dtype, m):
     assert torch.all(o[:, fill_to:] == 7.0)
 
 
-# 16 < M <= 64 on the streaming sign kernel (x staged per k-block with the pre scale applied,
-# K split over workgroups with an ordered reduce) and, pinned, on the large-M GEMM core (64-row
-# tiles, K split with fp32 partials and a fixup): pre and post scales, bias, fill_to of the rank
-# stage, a rank stage of one-k-block units, bf16.
-@pytest.mark.parametrize("m", [17, 32, 48, 64])
+# 13 <= M <= 64 on the streaming sign kernel (x staged per k-block with the pre scale applied,
+# two k-blocks per step up to 32 rows — an odd k-block count leaves the last step half past the
+# split — K split over workgroups with an ordered reduce) and, pinned, on the large-M GEMM core
+# (64-row tiles, K split with fp32 partials and a fixup): pre and post scales, bias, fill_to of the
+# rank stage, a rank stage of one-k-block units, bf16, row counts at and past each row-block size.
+@pytest.mark.parametrize("m", [13, 16, 17, 32, 33, 48, 63, 64])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("path", ["stream", "gemm", "stream_s1", "stream_s3"])
 def test_dbf_mid_m(dev, m, dtype, path, plan):
