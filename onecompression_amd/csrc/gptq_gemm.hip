@@ -1120,7 +1120,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
   int ntc[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) ntc[j] = min(nt0 + j, a.NT_total - 1);  // past the last n-tile: computed, unused
-  const int M = a.M;
+  // rows of this workgroup: blockIdx.z's block of 16 MB rows (one block unless the rows are split
+  // across workgroups as well)
+  const int m0 = blockIdx.z * 16 * MB;
+  const int M = min(a.M - m0, 16 * MB);
   // this split's units (a multiple of D: the planner keeps NU / S even)
   const int split = blockIdx.y;
   const int nu = a.NU / a.S, ub = split * nu;
@@ -1129,7 +1132,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
   float* xsum = (float*)(xl + 2 * ROWS * XLD);     // [2][ROWS] (SUMS only)
 
   // staging of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at 8 (c % 16))
-  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.x, (uint32_t)M * a.K * 2);
+  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(a.x + (size_t)m0 * a.K, (uint32_t)M * a.K * 2);
   oc_u4 xs_reg[MB];
   auto stage_load = [&](int kb) {
 #pragma unroll
@@ -1278,7 +1281,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
     const int n = (nt0 + j) * 16 + col;
     if (nt0 + j >= a.NT_total || n >= a.N) continue;
     if (a.S > 1) {
-      float* pp = a.partial + (size_t)split * M * a.N_pad + n;
+      float* pp = a.partial + ((size_t)split * a.M + m0) * a.N_pad + n;
 #pragma unroll
       for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -1294,7 +1297,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const StreamArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 16 * i + 4 * kq + r;
-        if (m < M) a.y[(size_t)m * a.ldy + n] = BF16 ? oc_f2bf(yacc[i][j][r] + b) : oc_f2h(yacc[i][j][r] + b);
+        if (m < M) a.y[(size_t)(m0 + m) * a.ldy + n] = BF16 ? oc_f2bf(yacc[i][j][r] + b) : oc_f2h(yacc[i][j][r] + b);
       }
   }
 }
@@ -1512,15 +1515,16 @@ bool use_gemm_stream(const oc::Layout& L, int M, int gs) {
   return L.NT >= 1024 && (M > 12 || (size_t)M * (L.K_pad + 8) * 2 + (size_t)(L.K_pad / 128) * 64 > 80 * 1024);
 }
 
-// K splits of k_gemm_stream (workgroups of 4 NTW n-tiles): enough workgroups
-// for one per CU (two per CU on layers of >= 64 k-blocks), at most 8 splits, at
+// K splits of k_gemm_stream (workgroups of 4 NTW n-tiles, times the row blocks):
+// enough workgroups for one per CU (two per CU on layers of >= 64 k-blocks or
+// with the rows split), at most 8 splits, at
 // least 4 k-blocks per split, none when the column workgroups cover 3/4 of the
 // CUs, and an even number of units per split.
 // OC_GEMM_STREAM_S forces the count.
-int gemm_stream_split(const oc::Layout& L, int ntw) {
+int gemm_stream_split(const oc::Layout& L, int ntw, int mz) {
   const int e = oc::knob("OC_GEMM_STREAM_S", 0);
-  const int wgs = (L.NT + 4 * ntw - 1) / (4 * ntw), nkb = L.K_pad / 128;
-  const int target = oc_device_cus() * (nkb >= 64 ? 2 : 1);
+  const int wgs = (L.NT + 4 * ntw - 1) / (4 * ntw) * mz, nkb = L.K_pad / 128;
+  const int target = oc_device_cus() * ((nkb >= 64 || mz > 1) ? 2 : 1);
   int S = e > 0 ? e : (target + wgs - 1) / wgs;
   if (e <= 0) {
     if (S > 8) S = 8;
@@ -1549,10 +1553,38 @@ int gemm_stream_ntw(const oc::Layout& L, int M) {
   return L.NT >= 512 ? 2 : 1;
 }
 
+// Row blocks of k_gemm_stream across workgroups (grid.z): above 64 rows two (64-row halves:
+// twice the workgroups, each with half the MFMA chain and LDS traffic per k-block, two per CU to
+// hide each other's step latency; the weights are read twice, from L2).  Measured (graph of 32
+// calls, µs): config 1 q/o M = 128 19.4 -> 17.2, k|v 13.2 -> 11.1, gate 38.2 -> 29.3; config 2
+// gate 39.9 -> 32.8.  OC_GEMM_STREAM_MZ = 1 or 2 forces the count there.
+int gemm_stream_mz(const oc::Layout& L, int M) {
+  (void)L;
+  if (M <= 64) return 1;
+  const int e = oc::knob("OC_GEMM_STREAM_MZ", 0);
+  if (e == 1 || e == 2) return e;
+  return 2;
+}
+
+struct GemmStreamPlan {
+  int mz, mb, ntw, S;  // row blocks across workgroups, row blocks of 16 per workgroup, n-tiles per wave, K splits
+};
+
+GemmStreamPlan plan_gemm_stream(const oc::Layout& L, int M) {
+  GemmStreamPlan p;
+  p.mz = gemm_stream_mz(L, M);
+  const int mr = (M + p.mz - 1) / p.mz;
+  p.mb = gemm_stream_rows(mr);
+  p.ntw = gemm_stream_ntw(L, mr);
+  p.S = gemm_stream_split(L, p.ntw, p.mz);
+  return p;
+}
+
 template <bool BF16>
 int dispatch_gemm_stream(int bits, int M, const oc::Layout& L, const StreamArgs& a, hipStream_t st) {
-  const int mbt = gemm_stream_rows(M), ntw = gemm_stream_ntw(L, M);
-  const dim3 grid((L.NT + 4 * ntw - 1) / (4 * ntw), a.S), block(256);
+  const GemmStreamPlan sp = plan_gemm_stream(L, M);
+  const int mz = sp.mz, mbt = sp.mb, ntw = sp.ntw;
+  const dim3 grid((L.NT + 4 * ntw - 1) / (4 * ntw), a.S, mz), block(256);
   const size_t lds = (size_t)2 * 16 * mbt * 136 * 2 + (mbt <= 2 ? (size_t)2 * 16 * mbt * 4 : 0);
 #define OC_GS(B_, MB_, NTW_)                                                                \
   if (bits == B_ && mbt == MB_ && ntw == NTW_) {                                            \
@@ -1678,7 +1710,7 @@ extern "C" size_t oc_gptq_workspace_bytes(int M, int K, int N, int bits, int gro
   const int gs = oc::eff_group(group_size, K);
   if (M <= kGemvMaxM && stream_depth(L, M, gs) > 0) return ws;
   if (use_gemm_stream(L, M, gs)) {
-    const int S = gemm_stream_split(L, gemm_stream_ntw(L, M));
+    const int S = plan_gemm_stream(L, M).S;
     return S > 1 ? ws + align256((size_t)S * M * L.N_pad * 4) : ws;
   }
   if (M <= kGemvMaxM) {
@@ -1706,8 +1738,9 @@ extern "C" int oc_gptq_describe_plan(int M, int K, int N, int bits, int group_si
   const char* g = has_perm ? "k_gather + " : "";
   const int sd = M <= kGemvMaxM ? stream_depth(L, M, gs) : 0;
   if (sd == 0 && use_gemm_stream(L, M, gs)) {
-    const int S = gemm_stream_split(L, gemm_stream_ntw(L, M));
-    snprintf(buf, len, "%sk_gemm_stream mb=%d ntw=%d S=%d%s", g, gemm_stream_rows(M), gemm_stream_ntw(L, M), S,
+    const GemmStreamPlan sp = plan_gemm_stream(L, M);
+    const int S = sp.S;
+    snprintf(buf, len, "%sk_gemm_stream mz=%d mb=%d ntw=%d S=%d%s", g, sp.mz, sp.mb, sp.ntw, S,
              S > 1 ? " + k_splitk_reduce" : "");
   } else if (M <= kGemvMaxM && sd > 0) {
     const int t = stream_bal_tiles(L, bits, M, stream_ksplit(L));
@@ -1777,7 +1810,7 @@ int gptq_gemm_impl(const void* x, int M, int K, int N, const void* packed, const
     a.gs = gs;
     a.gkb_shift = log2_exact(gs) - 7;
     a.ldy = ldy;
-    a.S = gemm_stream_split(L, gemm_stream_ntw(L, M));
+    a.S = plan_gemm_stream(L, M).S;
     a.partial = (float*)ws;
     const int rc = bf16 ? dispatch_gemm_stream<true>(bits, M, L, a, st) : dispatch_gemm_stream<false>(bits, M, L, a, st);
     if (rc || a.S == 1) return rc;

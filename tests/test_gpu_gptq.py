@@ -381,6 +381,19 @@ def test_gemm_stream_mid_m_split(dev, bits, m, split, ntw, plan):
     _gemm_check(dev, _case(2048, n, bits, seed=400 + 7 * bits + m + split), m, "fp16", bias=(split == 2), tol=2e-3)
 
 
+# Rows split across workgroups as well (grid.z = 64-row halves, each with its own x slice, output
+# rows and partial rows), with and without K splits; a ragged second half.
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("m", [65, 100, 128])
+@pytest.mark.parametrize("split", [1, 2, 4])
+def test_gemm_stream_row_split(dev, bits, m, split, plan):
+    plan("OC_GEMM_STREAM", 1)
+    plan("OC_GEMM_STREAM_MZ", 2)
+    plan("OC_GEMM_STREAM_S", split)
+    n = 720 if bits != 3 else 736
+    _gemm_check(dev, _case(2048, n, bits, seed=470 + 7 * bits + m + split), m, "fp16", bias=(split == 1), tol=2e-3)
+
+
 # The tiled GEMM at the mid M the streaming GEMM now serves (64-row tiles, K split pieces).
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("m", [33, 64, 100])
