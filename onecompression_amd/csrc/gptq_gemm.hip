@@ -1560,10 +1560,10 @@ int gemm_stream_ntw(const oc::Layout& L, int M) {
 // gate 39.9 -> 32.8.  OC_GEMM_STREAM_MZ = 1 or 2 forces the count there.
 int gemm_stream_mz(const oc::Layout& L, int M) {
   (void)L;
-  if (M <= 64) return 1;
+  if (M <= 32) return 1;
   const int e = oc::knob("OC_GEMM_STREAM_MZ", 0);
   if (e == 1 || e == 2) return e;
-  return 2;
+  return M > 64 ? 2 : 1;
 }
 
 struct GemmStreamPlan {
