@@ -1559,11 +1559,14 @@ int gemm_stream_ntw(const oc::Layout& L, int M) {
 // calls, µs): config 1 q/o M = 128 19.4 -> 17.2, k|v 13.2 -> 11.1, gate 38.2 -> 29.3; config 2
 // gate 39.9 -> 32.8.  OC_GEMM_STREAM_MZ = 1 or 2 forces the count there.
 int gemm_stream_mz(const oc::Layout& L, int M) {
-  (void)L;
   if (M <= 32) return 1;
   const int e = oc::knob("OC_GEMM_STREAM_MZ", 0);
   if (e == 1 || e == 2) return e;
-  return M > 64 ? 2 : 1;
+  if (M <= 64) return 1;
+  // not where the column workgroups alone cover 3/4 of the CUs: there the second half only
+  // doubles the weight reads (config-1 merged gate|up M = 128: 49.1 -> 52.1 us, 55 -> 72 MB)
+  const int ntw = gemm_stream_ntw(L, 64), wgs = (L.NT + 4 * ntw - 1) / (4 * ntw);
+  return 4 * wgs >= 3 * oc_device_cus() ? 1 : 2;
 }
 
 struct GemmStreamPlan {
