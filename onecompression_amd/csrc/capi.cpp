@@ -33,7 +33,7 @@ static const char* const kKnobNames[] = {
     "OC_GEMV_STREAM_BAL", "OC_GEMM_STREAM", "OC_GEMM_MT",        "OC_GEMM_MIN_M", "OC_GEMM_SPLIT",
     "OC_GROUP_NT",       "OC_MOE_RM",      "OC_MOE_W2",          "OC_MOE_GEMM",   "OC_MOE_GEMM_MT",
     "OC_SIGN_W",         "OC_SIGN_GEMM_MIN_M", "OC_HAD_MM_M",    "OC_SIGN_PLAN",  "OC_GEMM_PLAN",
-    "OC_GEMM_STREAM_S", "OC_GEMM_STREAM_NTW", "OC_GEMM_STREAM_MZ", "OC_SIGN_STREAM", "OC_SIGN_STREAM_S"};
+    "OC_GEMM_STREAM_S", "OC_GEMM_STREAM_NTW", "OC_GEMM_STREAM_MZ", "OC_SIGN_STREAM", "OC_SIGN_STREAM_S", "OC_SIGN_STREAM_MZ"};
 constexpr int kKnobs = (int)(sizeof(kKnobNames) / sizeof(kKnobNames[0]));
 static int g_knob_val[kKnobs];
 static bool g_knob_set[kKnobs];

@@ -493,6 +493,7 @@ struct SignStreamArgs {
   uint16_t* outs[kMaxTerms];
   float* partial;         // [T S, M, N_pad] when the outputs take more than one partial
   int ld_out, M, R, RT, S, T, fill_to, N_pad, separate;
+  int mz;  // row blocks across workgroups (grid.z; host only)
 };
 
 
@@ -520,7 +521,10 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   const int ups = (NU + a.S - 1) / a.S;
   const int u0 = split * ups, u1 = min(u0 + ups, NU);
   const int kb0 = u0 * UK, kb1 = u1 * UK;
-  const int M = a.M;
+  // rows of this workgroup: blockIdx.z's block of 16 MB rows (one block unless the rows are split
+  // across workgroups as well)
+  const int m0 = blockIdx.z * 16 * MB;
+  const int M = min(a.M - m0, 16 * MB);
   const uint32_t one2 = oc_opaque(BF16 ? 0x3F803F80u : 0x3C003C00u);
   const uint32_t smask = oc_opaque(0x80008000u);
 
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   // x of k-block kb: thread t owns chunks c = t + 256 j (row c / 16, 8 k at
   // 8 (c % 16)); chunks at k >= Kd, rows >= M and k-blocks past the split read
   // zero (offsets past the descriptors, no memory access)
-  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(in, (uint32_t)M * ld_in * 2);
+  const __amdgpu_buffer_rsrc_t xr = oc_rsrc(in + (size_t)m0 * ld_in, (uint32_t)M * ld_in * 2);
   const __amdgpu_buffer_rsrc_t pr = oc_rsrc(pre, (uint32_t)((Kd + 7) / 8 * 8) * 2);
   const int ck = 8 * (threadIdx.x & 15);
   oc_u4 xq[XL][MB], pq[XL];  // slot j % XL: x (and pre) of k-block j of the period
@@ -644,7 +648,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
   if (n < a.R) ps = post ? (BF16 ? oc_bf2f(post[n]) : oc_h2f(post[n])) : 1.f;
   uint16_t* const out = a.separate ? term_pick(t, a.outs) : a.outs[0];
   if ((a.separate ? a.S : a.S * a.T) > 1) {
-    float* pp = a.partial + (size_t)blockIdx.y * M * a.N_pad + n;
+    float* pp = a.partial + ((size_t)blockIdx.y * a.M + m0) * a.N_pad + n;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -660,7 +664,7 @@ __global__ __launch_bounds__(256, 2) void k_sign_stream(const SignStreamArgs a) 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 16 * i + 4 * kq + r;
-      if (m < M) out[(size_t)m * a.ld_out + n] = BF16 ? oc_f2bf(fmaf(yacc[i][r], ps, b)) : oc_f2h(fmaf(yacc[i][r], ps, b));
+      if (m < M) out[(size_t)(m0 + m) * a.ld_out + n] = BF16 ? oc_f2bf(fmaf(yacc[i][r], ps, b)) : oc_f2h(fmaf(yacc[i][r], ps, b));
     }
 }
 
@@ -687,7 +691,8 @@ __global__ void k_sign_reduce(const SignReduceArgs a) {
 
 struct SignStreamPlan {
   bool use;
-  int mb, S, T;   // row blocks, K splits per term, terms
+  int mb, S, T;   // row blocks of 16 per workgroup, K splits per term, terms
+  int mz;         // row blocks across workgroups (grid.z)
   bool separate;  // terms into their own outputs (a batch of problems)
   size_t bytes;   // fp32 partials when an output takes more than one (+ k_sign_reduce)
 };
@@ -712,17 +717,31 @@ SignStreamPlan plan_sign_stream(const oc_sign_term* terms, int n_terms, int M, i
     if (Li.NU < nu_min) nu_min = Li.NU;
   }
   if (!p.use) return p;
-  p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  const int nkb = nu_min * L.UK, wgs = (L.RT + 3) / 4 * n_terms;  // workgroups per split
-  const int es = oc::knob("OC_SIGN_STREAM_S", 0);
-  int S = es > 0 ? es : (oc_device_cus() + wgs - 1) / wgs;
-  if (es <= 0) {
-    if (S > 8) S = 8;
-    if (S > nkb / 4) S = nkb / 4;
-    // column workgroups that already cover 3/4 of the CUs: no split (one
-    // term: no reduce launch; up_proj's output stage at M = 32: 23.8 -> 21.5 us)
-    if (4 * wgs >= 3 * oc_device_cus()) S = 1;
-  }
+  const int nkb = nu_min * L.UK, es = oc::knob("OC_SIGN_STREAM_S", 0);
+  auto splits = [&](int wgs) {  // wgs: workgroups per split
+    int S = es > 0 ? es : (oc_device_cus() + wgs - 1) / wgs;
+    if (es <= 0) {
+      if (S > 8) S = 8;
+      if (S > nkb / 4) S = nkb / 4;
+      // column workgroups that already cover 3/4 of the CUs: no split (one
+      // term: no reduce launch; up_proj's output stage at M = 32: 23.8 -> 21.5 us)
+      if (4 * wgs >= 3 * oc_device_cus()) S = 1;
+    }
+    return S;
+  };
+  const int wgs1 = (L.RT + 3) / 4 * n_terms;
+  // Rows split across workgroups as well (two row blocks, grid.z) where one term would run
+  // unsplit: twice the workgroups, each with half the step's MFMA chain, two per CU to hide
+  // each other's step latency; the signs are read twice, from L2 (up_proj's output stage at
+  // M = 32 / 48 / 64: 22.9 -> 21.3, 30.9 -> 27.6, 32.4 -> 29.5 us).  Where K splits already give
+  // the parallelism (rank stages, down_proj, MDBF) it measured slower.  OC_SIGN_STREAM_MZ = 1 or 2
+  // forces the count.
+  const int ez = oc::knob("OC_SIGN_STREAM_MZ", 0);
+  p.mz = M <= 16 ? 1 : (ez == 1 || ez == 2) ? ez : (n_terms == 1 && !separate && splits(wgs1) == 1 ? 2 : 1);
+  const int mr = (M + p.mz - 1) / p.mz;
+  p.mb = mr <= 16 ? 1 : (mr <= 32 ? 2 : 4);
+  const int wgs = wgs1 * p.mz;
+  int S = splits(wgs);
   if (S > nu_min) S = nu_min;
   if (S < 1) S = 1;
   p.S = S;
@@ -739,7 +758,7 @@ constexpr int sign_stream_kps(int mb) { return mb <= 2 ? 2 : 1; }
 
 template <int UK, bool BF16>
 int launch_sign_stream_uk(const SignStreamArgs& a, int mb, bool pre, hipStream_t st) {
-  const dim3 grid((a.RT + 3) / 4, a.S * a.T), block(256);
+  const dim3 grid((a.RT + 3) / 4, a.S * a.T, a.mz), block(256);
   const size_t lds = (size_t)2 * 16 * mb * (sign_stream_kps(mb) * 128 + 8) * 2;
 #define OC_SS(MB_)                                                                                         \
   if (mb == MB_) {                                                                                         \
@@ -791,6 +810,7 @@ int sign_stream(const oc_sign_term* terms, int M, int R, bool bf16, const void* 
   a.fill_to = fill_to;
   a.N_pad = L.RT * 16;
   a.separate = p.separate ? 1 : 0;
+  a.mz = p.mz;
   const bool pre = terms[0].pre != nullptr;
   const int rc = bf16 ? launch_sign_stream<true>(a, L.UK, p.mb, pre, st)
                 : launch_sign_stream<false>(a, L.UK, p.mb, pre, st);

@@ -181,10 +181,12 @@ def test_sign_gemm_fill_and_bias(dev, dtype, m):
 # rank stage, a rank stage of one-k-block units, bf16, row counts at and past each row-block size.
 @pytest.mark.parametrize("m", [13, 16, 17, 32, 33, 48, 63, 64])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-@pytest.mark.parametrize("path", ["stream", "gemm", "stream_s1", "stream_s3"])
+@pytest.mark.parametrize("path", ["stream", "gemm", "stream_s1", "stream_s3", "stream_mz2"])
 def test_dbf_mid_m(dev, m, dtype, path, plan):
     if path == "gemm":
         plan("OC_SIGN_STREAM", 0)
+    elif path == "stream_mz2":  # rows split across workgroups as well (two row blocks)
+        plan("OC_SIGN_STREAM_MZ", 2)
     elif path != "stream":
         plan("OC_SIGN_STREAM_S", int(path[-1]))
     k, n = 1408, 720  # r = 476: rank stage 30 tiles x 11 k-blocks, output stage 45 tiles x 4 k-blocks
