@@ -71,7 +71,11 @@ def test_dequant_config0_full_size_bit_exact(dev):
     assert np.array_equal(_np(got).view(np.uint16), _oracle_w(c, "fp16").view(np.uint16))
 
 
-def _gemm_check(dev, c, m, dtype, bias=False, tol=1e-2, seed=3):
+def _gemm_check(dev, c, m, dtype, bias=False, tol=None, seed=3):
+    # regression bounds well under the 1e-2 contract (the kernels measure ~3e-4 in fp16): fp16
+    # products are exact in fp32, the output rounds once; bf16 rounds its output at 2^-9
+    if tol is None:
+        tol = 2e-3 if dtype == "fp16" else 8e-3
     td = torch.float16 if dtype == "fp16" else torch.bfloat16
     cd = c.to(dev)
     prep = ops.gptq_prepare(cd.qweight, cd.qzeros, cd.scales, cd.g_idx, c.bits, c.group_size)
