@@ -437,16 +437,22 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   // every body issues the same instructions: the compiler's own waits stay
   // exact and never fall back to waiting for everything.
   const int last = kb1 - 1;
+  // tail = one of the bodies after the loop: their prefetched weights are never used, so the
+  // compiler deletes those loads and vmcnt(NW) would leave NW of the x-tile loads in flight
+  // across the barrier (the next body would read stale x); they wait for everything instead.
   auto body = [&](int kb, const uint32_t (&wc)[2][2][NWB], const uint32_t (&mc)[2][SPK],
                   const uint32_t (&wn)[2][2][NWB], const uint32_t (&mn)[2][SPK], uint32_t (&wf)[2][2][NWB],
-                  uint32_t (&mf)[2][SPK]) {
+                  uint32_t (&mf)[2][SPK], const bool tail) {
     const int buf = (kb - kb0) & 1;
     load_x(min(kb + 1, last), buf ^ 1);
     __builtin_amdgcn_sched_barrier(0);
     load_w(min(kb + 2, last), wf, mf);
     __builtin_amdgcn_sched_barrier(0);
     compute(buf, wc, mc, B0, dq);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NW) : "memory");
+    if (tail)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NW) : "memory");
     make_b(wn, mn, 0, B0, dq);
     // Plain s_barrier: __syncthreads() adds a workgroup release fence, which
     // waits for every outstanding load (vmcnt(0)) including k-block kb + 2.
@@ -465,12 +471,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm(const GemmArgs a) {
   __syncthreads();
   const int nkb = kb1 - kb0, groups = nkb / 3;
   for (int g = 0; g < groups; ++g) {
-    body(kb0 + 3 * g, w0, m0w, w1, m1w, w2, m2w);
-    body(kb0 + 3 * g + 1, w1, m1w, w2, m2w, w0, m0w);
-    body(kb0 + 3 * g + 2, w2, m2w, w0, m0w, w1, m1w);
+    body(kb0 + 3 * g, w0, m0w, w1, m1w, w2, m2w, false);
+    body(kb0 + 3 * g + 1, w1, m1w, w2, m2w, w0, m0w, false);
+    body(kb0 + 3 * g + 2, w2, m2w, w0, m0w, w1, m1w, false);
   }
-  if (nkb % 3 >= 1) body(kb0 + 3 * groups, w0, m0w, w1, m1w, w2, m2w);
-  if (nkb % 3 == 2) body(kb0 + 3 * groups + 1, w1, m1w, w2, m2w, w0, m0w);
+  if (nkb % 3 >= 1) body(kb0 + 3 * groups, w0, m0w, w1, m1w, w2, m2w, true);
+  if (nkb % 3 == 2) body(kb0 + 3 * groups + 1, w1, m1w, w2, m2w, w0, m0w, true);
   // the last body prefetched into the idle x buffer: let it land before exit
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 

@@ -2495,9 +2495,9 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
     a.ups = L.NU;
     a.bits = bits;
   };
-  // The grouped large-M GEMM per run of rows (prefill sizes) is opt-in (knob OC_MOE_GEMM = 1):
-  // one test run of it once reported a wrong result whose cause has not been shown, so the
-  // default serves every size on the sorted-run GEMV path.
+  // The grouped large-M GEMM per run of rows (prefill sizes) is opt-in (knob OC_MOE_GEMM = 1).
+  // Its one wrong result came from the GEMM core's tail hand-off, since fixed (gemm_core.h); the
+  // default serves every size on the sorted-run GEMV path until it has a record under the fix.
   {
     const int gm = oc::knob("OC_MOE_GEMM", 0);
     if (E <= kMoeMaxE && pairs >= 32 && gm == 1 && !act_order)
