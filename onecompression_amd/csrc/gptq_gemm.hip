@@ -2495,14 +2495,15 @@ extern "C" int oc_moe_gptq_forward(const void* x, int M, int H, int I, int E, in
     a.ups = L.NU;
     a.bits = bits;
   };
-  // The grouped large-M GEMM per run of rows (prefill sizes) serves at least 128 rows per busy
-  // expert on average (measured: Qwen3-30B-A3B experts at M = 2048 1053 -> 430 us, Mixtral-8x7B
-  // at M = 512 1782 -> 660 us); fewer rows take the sorted-run GEMV path.  OC_MOE_GEMM = 1 forces
-  // it from 32 pairs, = 0 turns it off.
+  // The grouped large-M GEMM per run of rows (prefill sizes) serves at least 32 rows per busy
+  // expert on average (measured against the sorted-run GEMV path, us: Qwen3-30B-A3B experts
+  // M = 512 325 -> 157, M = 2048 1053 -> 430; Mixtral-8x7B M = 128 527 -> 309, M = 512 1782 ->
+  // 660); fewer rows take the sorted-run path.  OC_MOE_GEMM = 1 forces it from 32 pairs, = 0
+  // turns it off.
   {
     const int gm = oc::knob("OC_MOE_GEMM", -1);
     const int busy = E < pairs ? E : pairs;
-    const bool on = gm == 1 || (gm < 0 && busy > 0 && pairs / busy >= 128);
+    const bool on = gm == 1 || (gm < 0 && busy > 0 && pairs / busy >= 32);
     if (E <= kMoeMaxE && pairs >= 32 && on && !act_order)
       return moe_prefill(x, M, H, I, E, topk, ids, weights, w13, w13_stride, meta13, meta13_stride, b13, w2,
                          w2_stride, meta2, meta2_stride, b2, bits, gs13, gs2, act, alpha, limit, bf16, y, ws, mp, st);
